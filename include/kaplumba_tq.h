@@ -1,0 +1,150 @@
+/*
+ * kaplumba_tq.h -- C ABI of the MI355X TurboQuant KV-cache library
+ * (libkaplumba_tq.so, hand-written HIP kernels for gfx950).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * passed as void*, returns a status code (0 = success) and never throws.
+ * Work is enqueued asynchronously on the given stream; all buffers are
+ * caller-allocated device memory.  No entry point allocates device memory.
+ *
+ * Layouts (row-major, innermost last):
+ *   input vectors x      : [B, H, L, dim] with element strides (sb, sh, sl), last dim contiguous
+ *   packed indices       : [B, H, capacity, PW] uint32, PW = ceil(dim*bits/32),
+ *                          LSB-first bit stream: element i occupies bits i*bits.. of the row
+ *   norms                : [B, H, capacity] float32 or float16
+ *   plain (fp16/bf16) KV : [B, H, capacity, dim]
+ *   attention output     : [B, Hq, L, dim] in the query dtype
+ *
+ * The reference is the mlx-lm TurboQuant cache of zayutaha/kaplumba,
+ * mlx_lm/models/turboquant_cache.py (cited below as tq.py) and
+ * mlx_lm/models/base.py / cache.py.  The reference is Python calling Metal
+ * kernels through mx.fast.metal_kernel; a maintainer binds these symbols with
+ * ctypes (see kaplumba_amd/_lib.py).
+ */
+#ifndef KAPLUMBA_TQ_H
+#define KAPLUMBA_TQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+  TQ_OK = 0,
+  TQ_ERR_INVALID_ARGUMENT = 1, /* bad shape, bits, dtype, null pointer, ... */
+  TQ_ERR_UNSUPPORTED = 2,      /* valid request outside the compiled kernel set */
+  TQ_ERR_WORKSPACE = 3,        /* workspace smaller than tq_attention_workspace_size() */
+  TQ_ERR_HIP = 4               /* a HIP runtime call failed (message has the HIP error) */
+};
+
+/* ---- enums ------------------------------------------------------------- */
+enum { TQ_DTYPE_F32 = 0, TQ_DTYPE_F16 = 1, TQ_DTYPE_BF16 = 2 };
+enum { TQ_ROT_HADAMARD = 0, TQ_ROT_DENSE = 1 };
+enum { TQ_KV_PACKED = 0, TQ_KV_PLAIN = 1 };
+
+/* Library version string, e.g. "kaplumba_tq 0.1.0 gfx950". */
+const char* tq_version(void);
+
+/* Human-readable message for the last failing call on this host thread. */
+const char* tq_last_error(void);
+
+/* Packed row width in uint32 words: ceil(dim*bits/32)
+ * (replaces _packed_width, tq.py:3699-3702). */
+int tq_packed_width(int dim, int bits);
+
+/*
+ * Append-time quantization of L new tokens per (batch, head).
+ *
+ * Replaces _TurboQuantMSECodec.quantize (tq.py:4186-4254) together with
+ * _write_state (tq.py:3978-3986) as used by TurboQuantKVCache.update_and_fetch
+ * (tq.py:5026-5064): for every vector x,
+ *   n = ||x||_2 (f32), u = x / max(n, 1e-6),
+ *   y = H(s * u) / sqrt(dim)   (rot_kind TQ_ROT_HADAMARD, rot = s: dim floats)
+ *   y = u @ R^T                (rot_kind TQ_ROT_DENSE, rot = R: dim*dim floats, row-major)
+ *   idx_i = #{ m : y_i > midpoints[m] }   (2^bits - 1 ascending midpoints)
+ * and writes the packed row and the norm at token position offset + l of the
+ * (b, h) row of the destination buffers (capacity tokens per (b, h)).
+ * Hadamard: dim a power of two in [32, 512].  Dense: dim in {64, 128, 256}.
+ * bits in 1..4.  x_dtype: F32/F16/BF16.  norm_dtype: F32 or F16.
+ */
+int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
+                       int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
+                       int bits, int rot_kind, const float* rot, const float* midpoints,
+                       uint32_t* packed, void* norms, int norm_dtype,
+                       int64_t capacity, int64_t offset, void* stream);
+
+/*
+ * Append L tokens unquantized into an fp16/bf16 layer buffer (the
+ * mixed-precision layers).  Replaces the slice assignment of
+ * KVCache.update_and_fetch (cache.py:415-441).  dtype: F16 or BF16; x and dst
+ * share it.  dst is [B, H, capacity, dim].
+ */
+int tq_append_plain(const void* x, int dtype, int B, int H, int L, int dim,
+                    int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
+                    void* dst, int64_t capacity, int64_t offset, void* stream);
+
+/*
+ * Unpack and dequantize vectors: out[b,h,t,:] = n * R^-1(codebook[idx]),
+ * f32 output [B, H, T, dim] for tokens 0..T-1.  Replaces
+ * TurboQuantKVCache.dequantize (tq.py:5070-5077).  Used by tests and by the
+ * cache's dequantize() API, not by attention.
+ */
+int tq_dequantize(const uint32_t* packed, const void* norms, int norm_dtype,
+                  int B, int H, int T, int dim, int bits, int64_t capacity,
+                  const float* codebook, int rot_kind, const float* rot,
+                  float* out, void* stream);
+
+/*
+ * Bytes of workspace tq_attention() needs for this problem (split-K partials,
+ * rotated queries and merge counters).  max_tokens is the largest
+ * per-sequence cache length.
+ */
+int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
+                                    int64_t max_tokens);
+
+/*
+ * Decode / speculative-verify attention straight from the cache.
+ *
+ * Replaces TurboQuantKVCache.decode_attention (tq.py:5776-5947) for L == 1,
+ * the dequantize + SDPA fallback of scaled_dot_product_attention
+ * (base.py:177-189) for L > 1, and the plain SDPA of the fp16 layers
+ * (base.py:218-226).  Semantics follow quantized_attention (tq.py:5110-5203):
+ *   q_s   = round_qdtype(q * round_qdtype(scale))
+ *   q_rot = R_K(q_s)
+ *   s_t   = n_k[t] * <q_rot, codebook_k[idx_k[t]]>         (packed)
+ *   s_t   = <q_s, k[t]>                                     (plain)
+ *   causal: query row l of L sees keys t <= T_b - L + l, others get -FLT_MAX
+ *   o     = R_V^-1( sum_t p_t n_v[t] codebook_v[idx_v[t]] ) / max(sum_t p_t, 1e-6)
+ * GQA: query head h reads kv head h / (Hq / Hkv).
+ * kv_kind TQ_KV_PACKED: k/v are packed uint32 rows, k_norms/v_norms given,
+ *   norm_dtype F32/F16, bits 1..4 each, rot_kind selects R_K/R_V as in append.
+ * kv_kind TQ_KV_PLAIN: k/v are [B, Hkv, capacity, dim] in kv_dtype (F16/BF16);
+ *   norms, codebooks and rotations are ignored (may be NULL).
+ * seq_lens: NULL (every sequence holds max_tokens tokens) or a device int32
+ *   array of B lengths, each <= max_tokens (ragged batches).
+ * q: [B, Hq, L, dim] with element strides; out: contiguous [B, Hq, L, dim].
+ * dim in {64, 128, 256}; L >= 1; Hq % Hkv == 0.
+ * workspace: >= tq_attention_workspace_size() bytes, 256-byte aligned.  Its
+ *   first 64 KiB hold merge counters that must be zero before the first call
+ *   that uses this workspace (zero it once, e.g. with hipMemset); every call
+ *   leaves them zero again, whatever the shapes of later calls.  Calls that
+ *   may run concurrently (other streams) must use different workspaces.
+ */
+int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                 int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
+                 int kv_kind, int kv_dtype,
+                 const void* k, const void* k_norms, const void* v, const void* v_norms,
+                 int norm_dtype, int k_bits, int v_bits,
+                 const float* k_codebook, const float* v_codebook,
+                 int rot_kind, const float* k_rot, const float* v_rot,
+                 int64_t capacity, int64_t max_tokens, const int32_t* seq_lens, int causal,
+                 void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KAPLUMBA_TQ_H */

@@ -1,0 +1,377 @@
+// Append-time kernels: TurboQuant quantize + pack (randomized Hadamard),
+// unquantized append for the fp16/bf16 layers, and dequantize.
+//
+// Quantize follows _TurboQuantMSECodec.quantize (turboquant_cache.py:4186-4254)
+// with one fixed fp32 operation order that the CPU oracle reproduces bit for
+// bit:
+//   * lane g of a vector owns elements [32g, 32g+32) (D/32 lanes per vector);
+//   * ||x||^2: a lane squares its 32 elements and folds them at distances
+//     16, 8, 4, 2, 1, then lanes combine by xor-butterfly 1, 2, 4 ...;
+//   * n = sqrt (IEEE, correctly rounded), u = x / max(n, 1e-6) (IEEE division);
+//   * Walsh-Hadamard butterflies at distances 1, 2, ..., D/2, each mapping
+//     (a, b) -> (a + b, a - b); distances < 32 run inside a lane, the rest
+//     across lanes with shuffles;
+//   * y = v * f32(1/sqrt(D)); idx = #{m : y > mid[m]} (strict compare);
+//   * a lane's 32 indices fill exactly `bits` consecutive words of the
+//     LSB-first stream, so packing is thread-local (no shared-word races).
+#include "tq_common.h"
+
+namespace tq {
+
+struct AppendArgs {
+  const void* x;
+  int64_t sb, sh, sl;  // element strides of x
+  int B, H, L;
+  const float* rot;    // signs (D)
+  const float* mid;    // 2^bits - 1 midpoints
+  uint32_t* packed;
+  void* norms;
+  int norm_dtype;
+  int64_t cap, offset;
+  float scale;         // f32(1/sqrt(D))
+};
+
+// Load 32 consecutive elements of dtype DT starting at p (16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load32(const void* p, float (&v)[32]) {
+  if constexpr (DT == TQ_DTYPE_F32) {
+    const float4* q = static_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float4 t = q[i];
+      v[4 * i + 0] = t.x;
+      v[4 * i + 1] = t.y;
+      v[4 * i + 2] = t.z;
+      v[4 * i + 3] = t.w;
+    }
+  } else {
+    const uint4* q = static_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint4 t = q[i];
+      uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = static_cast<uint16_t>(w[j] & 0xffffu);
+        const uint16_t hi = static_cast<uint16_t>(w[j] >> 16);
+        if constexpr (DT == TQ_DTYPE_F16) {
+          v[8 * i + 2 * j] = f16_bits_to_f32(lo);
+          v[8 * i + 2 * j + 1] = f16_bits_to_f32(hi);
+        } else {
+          v[8 * i + 2 * j] = bf16_bits_to_f32(lo);
+          v[8 * i + 2 * j + 1] = bf16_bits_to_f32(hi);
+        }
+      }
+    }
+  }
+}
+
+template <int D, int BITS, int XDT>
+__global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
+  constexpr int NL = D / 32;          // lanes per vector
+  constexpr int VPB = 256 / NL;       // vectors per block
+  constexpr int NMID = (1 << BITS) - 1;
+  constexpr int PW = D * BITS / 32;
+  __shared__ float s_sign[D];
+  __shared__ float s_mid[NMID];
+  for (int i = threadIdx.x; i < D; i += blockDim.x) s_sign[i] = a.rot[i];
+  if (threadIdx.x < NMID) s_mid[threadIdx.x] = a.mid[threadIdx.x];
+  __syncthreads();
+
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  const int64_t vec = static_cast<int64_t>(blockIdx.x) * VPB + threadIdx.x / NL;
+  const int g = threadIdx.x % NL;
+  // Every lane of a vector shares `vec`, so a vector's lanes leave together
+  // and the xor-shuffles below stay inside live lane groups.
+  if (vec >= n_vec) return;
+  const int l = static_cast<int>(vec % a.L);
+  const int64_t bh = vec / a.L;
+  const int h = static_cast<int>(bh % a.H);
+  const int b = static_cast<int>(bh / a.H);
+
+  const int64_t xoff = b * a.sb + h * a.sh + l * a.sl + g * 32;
+  constexpr int ES = XDT == TQ_DTYPE_F32 ? 4 : 2;
+  float v[32];
+  load32<XDT>(static_cast<const char*>(a.x) + xoff * ES, v);
+
+  // ---- norm: in-lane fold 16, 8, 4, 2, 1 then cross-lane xor butterfly
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = __fadd_rn(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 16], v[i + 16]));
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1) {
+#pragma unroll
+    for (int i = 0; i < w; ++i) s[i] = __fadd_rn(s[i], s[i + w]);
+  }
+  float ss = s[0];
+#pragma unroll
+  for (int off = 1; off < NL; off <<= 1) ss = __fadd_rn(ss, __shfl_xor(ss, off, kWave));
+  const float n = sqrt_rn(ss);
+  const float den = fmaxf(n, kNormEps);
+
+  // ---- normalise and apply signs (multiplying by +-1 is exact)
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], den), s_sign[g * 32 + i]);
+
+  // ---- Walsh-Hadamard: in-lane stages (distance 1..16)
+#pragma unroll
+  for (int hstep = 1; hstep < 32; hstep <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if ((i & hstep) == 0) {
+        const float x0 = v[i];
+        const float x1 = v[i + hstep];
+        v[i] = __fadd_rn(x0, x1);
+        v[i + hstep] = __fsub_rn(x0, x1);
+      }
+    }
+  }
+  // ---- cross-lane stages (distance 32, 64, ...): lane bit j <-> element bit 5+j
+#pragma unroll
+  for (int off = 1; off < NL; off <<= 1) {
+    const bool upper = (g & off) != 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float p = __shfl_xor(v[i], off, kWave);
+      v[i] = upper ? __fsub_rn(p, v[i]) : __fadd_rn(v[i], p);
+    }
+  }
+
+  // ---- scale, quantize against midpoints, pack thread-locally
+  uint32_t words[BITS];
+#pragma unroll
+  for (int w = 0; w < BITS; ++w) words[w] = 0u;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float y = __fmul_rn(v[i], a.scale);
+    uint32_t idx = 0;
+#pragma unroll
+    for (int m = 0; m < NMID; ++m) idx += (y > s_mid[m]) ? 1u : 0u;
+    const int pos = i * BITS;
+    const int wi = pos >> 5;
+    const int sh = pos & 31;
+    words[wi] |= idx << sh;
+    if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
+  }
+
+  const int64_t row = (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l;
+  uint32_t* dst = a.packed + row * PW + g * BITS;
+#pragma unroll
+  for (int w = 0; w < BITS; ++w) dst[w] = words[w];
+  if (g == 0) {
+    if (a.norm_dtype == TQ_DTYPE_F16)
+      static_cast<uint16_t*>(a.norms)[row] = f32_to_f16_bits(n);
+    else
+      static_cast<float*>(a.norms)[row] = n;
+  }
+}
+
+// ------------------------------------------------------------------ plain ---
+struct PlainArgs {
+  const uint16_t* x;
+  int64_t sb, sh, sl;
+  int B, H, L, D;
+  uint16_t* dst;
+  int64_t cap, offset;
+};
+
+// One thread copies 8 elements (16 bytes); D is a multiple of 8.
+__global__ __launch_bounds__(256) void append_plain_kernel(PlainArgs a) {
+  const int per_row = a.D / 8;
+  const int64_t total = static_cast<int64_t>(a.B) * a.H * a.L * per_row;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = static_cast<int>(i % per_row);
+  const int64_t vec = i / per_row;
+  const int l = static_cast<int>(vec % a.L);
+  const int64_t bh = vec / a.L;
+  const int h = static_cast<int>(bh % a.H);
+  const int b = static_cast<int>(bh / a.H);
+  const uint4* src = reinterpret_cast<const uint4*>(a.x + b * a.sb + h * a.sh + l * a.sl) + c;
+  uint4* dst = reinterpret_cast<uint4*>(
+                   a.dst + ((static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l) * a.D) +
+               c;
+  *dst = *src;
+}
+
+// ------------------------------------------------------------- dequantize ---
+struct DequantArgs {
+  const uint32_t* packed;
+  const void* norms;
+  int norm_dtype;
+  int B, H, T, D, bits, PW;
+  int64_t cap;
+  const float* cb;
+  int rot_kind;
+  const float* rot;
+  float scale;
+  float* out;
+};
+
+// One block per vector; D threads (64..256).  Test/API path, not hot.
+__global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
+  __shared__ float y[256];
+  const int64_t vec = blockIdx.x;  // (b*H + h)*T + t
+  const int t = static_cast<int>(vec % a.T);
+  const int64_t bh = vec / a.T;
+  const int64_t row = bh * a.cap + t;
+  const int i = threadIdx.x;
+  const uint32_t* w = a.packed + row * a.PW;
+  const int pos = i * a.bits;
+  uint32_t idx = w[pos >> 5] >> (pos & 31);
+  if ((pos & 31) + a.bits > 32) idx |= w[(pos >> 5) + 1] << (32 - (pos & 31));
+  idx &= (1u << a.bits) - 1u;
+  y[i] = a.cb[idx];
+  __syncthreads();
+  float r;
+  if (a.rot_kind == TQ_ROT_HADAMARD) {
+    for (int hstep = 1; hstep < a.D; hstep <<= 1) {
+      float mine = y[i];
+      float other = y[i ^ hstep];
+      __syncthreads();
+      y[i] = (i & hstep) ? __fsub_rn(other, mine) : __fadd_rn(mine, other);
+      __syncthreads();
+    }
+    r = __fmul_rn(__fmul_rn(y[i], a.scale), a.rot[i]);
+  } else {
+    // x = y @ R : x[i] = sum_j y[j] R[j][i]
+    float acc = 0.f;
+    for (int j = 0; j < a.D; ++j) acc = fmaf(y[j], a.rot[static_cast<int64_t>(j) * a.D + i], acc);
+    r = acc;
+  }
+  const float nrm = load_norm(a.norms, a.norm_dtype, row);
+  a.out[vec * a.D + i] = nrm * r;
+}
+
+}  // namespace tq
+
+using namespace tq;
+
+namespace {
+
+template <int D, int BITS>
+int launch_append_rht_bits(int x_dtype, const AppendArgs& a, hipStream_t st) {
+  constexpr int NL = D / 32;
+  constexpr int VPB = 256 / NL;
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  const int64_t blocks = (n_vec + VPB - 1) / VPB;
+  if (blocks > 0x7fffffff) return fail(TQ_ERR_INVALID_ARGUMENT, "append: too many vectors");
+  dim3 grid(static_cast<unsigned>(blocks));
+  switch (x_dtype) {
+    case TQ_DTYPE_F32:
+      hipLaunchKernelGGL((append_rht_kernel<D, BITS, TQ_DTYPE_F32>), grid, dim3(256), 0, st, a);
+      break;
+    case TQ_DTYPE_F16:
+      hipLaunchKernelGGL((append_rht_kernel<D, BITS, TQ_DTYPE_F16>), grid, dim3(256), 0, st, a);
+      break;
+    case TQ_DTYPE_BF16:
+      hipLaunchKernelGGL((append_rht_kernel<D, BITS, TQ_DTYPE_BF16>), grid, dim3(256), 0, st, a);
+      break;
+    default:
+      return fail(TQ_ERR_INVALID_ARGUMENT, "append: x_dtype %d", x_dtype);
+  }
+  return check_launch("append_rht_kernel");
+}
+
+template <int D>
+int launch_append_rht(int bits, int x_dtype, const AppendArgs& a, hipStream_t st) {
+  switch (bits) {
+    case 1: return launch_append_rht_bits<D, 1>(x_dtype, a, st);
+    case 2: return launch_append_rht_bits<D, 2>(x_dtype, a, st);
+    case 3: return launch_append_rht_bits<D, 3>(x_dtype, a, st);
+    case 4: return launch_append_rht_bits<D, 4>(x_dtype, a, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "append: bits %d not in 1..4", bits);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+// Implemented in tq_append_dense.hip (matrix-core rotation).
+namespace tq {
+int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
+}
+
+extern "C" int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
+                                  int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
+                                  int bits, int rot_kind, const float* rot,
+                                  const float* midpoints, uint32_t* packed, void* norms,
+                                  int norm_dtype, int64_t capacity, int64_t offset,
+                                  void* stream) {
+  if (B < 0 || H < 0 || L < 0) return fail(TQ_ERR_INVALID_ARGUMENT, "append: negative shape");
+  if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "append: bits %d not in 1..4", bits);
+  if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: norm_dtype %d", norm_dtype);
+  if (x_dtype != TQ_DTYPE_F32 && x_dtype != TQ_DTYPE_F16 && x_dtype != TQ_DTYPE_BF16)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: x_dtype %d", x_dtype);
+  if (offset < 0 || offset + L > capacity)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: tokens [%lld, %lld) exceed capacity %lld",
+                (long long)offset, (long long)(offset + L), (long long)capacity);
+  if (static_cast<int64_t>(B) * H * L == 0) return TQ_OK;
+  if (!x || !rot || !midpoints || !packed || !norms)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: null pointer");
+  const int es = x_dtype == TQ_DTYPE_F32 ? 4 : 2;
+  if (!aligned16(x) || (x_stride_b * es) % 16 || (x_stride_h * es) % 16 || (x_stride_l * es) % 16)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: x and its strides must be 16-byte aligned");
+  AppendArgs a{x, x_stride_b, x_stride_h, x_stride_l, B, H, L, rot, midpoints, packed, norms,
+               norm_dtype, capacity, offset, 1.0f / sqrtf(static_cast<float>(dim))};
+  a.scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rot_kind == TQ_ROT_HADAMARD) {
+    switch (dim) {
+      case 32: return launch_append_rht<32>(bits, x_dtype, a, st);
+      case 64: return launch_append_rht<64>(bits, x_dtype, a, st);
+      case 128: return launch_append_rht<128>(bits, x_dtype, a, st);
+      case 256: return launch_append_rht<256>(bits, x_dtype, a, st);
+      case 512: return launch_append_rht<512>(bits, x_dtype, a, st);
+    }
+    return fail(TQ_ERR_UNSUPPORTED, "append: Hadamard rotation needs dim in {32..512} pow2, got %d", dim);
+  }
+  if (rot_kind == TQ_ROT_DENSE) return launch_append_dense(a, dim, bits, x_dtype, st);
+  return fail(TQ_ERR_INVALID_ARGUMENT, "append: rot_kind %d", rot_kind);
+}
+
+extern "C" int tq_append_plain(const void* x, int dtype, int B, int H, int L, int dim,
+                               int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
+                               void* dst, int64_t capacity, int64_t offset, void* stream) {
+  if (dtype != TQ_DTYPE_F16 && dtype != TQ_DTYPE_BF16)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: dtype %d (F16/BF16 only)", dtype);
+  if (B < 0 || H < 0 || L < 0 || dim <= 0 || dim % 8)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: bad shape (dim %% 8 == 0 required)");
+  if (offset < 0 || offset + L > capacity)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: tokens exceed capacity");
+  if (static_cast<int64_t>(B) * H * L == 0) return TQ_OK;
+  if (!x || !dst) return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: null pointer");
+  if (!aligned16(x) || !aligned16(dst) || (x_stride_b * 2) % 16 || (x_stride_h * 2) % 16 ||
+      (x_stride_l * 2) % 16)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: 16-byte alignment required");
+  PlainArgs a{static_cast<const uint16_t*>(x), x_stride_b, x_stride_h, x_stride_l, B, H, L, dim,
+              static_cast<uint16_t*>(dst), capacity, offset};
+  const int64_t total = static_cast<int64_t>(B) * H * L * (dim / 8);
+  hipLaunchKernelGGL(append_plain_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("append_plain_kernel");
+}
+
+extern "C" int tq_dequantize(const uint32_t* packed, const void* norms, int norm_dtype, int B,
+                             int H, int T, int dim, int bits, int64_t capacity,
+                             const float* codebook, int rot_kind, const float* rot, float* out,
+                             void* stream) {
+  if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: bits %d", bits);
+  if (dim < 32 || dim > 256 || (dim & (dim - 1)))
+    return fail(TQ_ERR_UNSUPPORTED, "dequantize: dim %d (pow2 32..256)", dim);
+  if (T < 0 || T > capacity) return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: T > capacity");
+  if (rot_kind != TQ_ROT_HADAMARD && rot_kind != TQ_ROT_DENSE)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: rot_kind %d", rot_kind);
+  const int64_t n = static_cast<int64_t>(B) * H * T;
+  if (n == 0) return TQ_OK;
+  if (!packed || !norms || !codebook || !rot || !out)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: null pointer");
+  DequantArgs a{packed, norms, norm_dtype, B, H, T, dim, bits, tq_packed_width(dim, bits),
+                capacity, codebook, rot_kind, rot,
+                static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim))), out};
+  hipLaunchKernelGGL(dequant_kernel, dim3(static_cast<unsigned>(n)), dim3(dim), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("dequant_kernel");
+}

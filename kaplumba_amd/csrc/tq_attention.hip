@@ -1,0 +1,197 @@
+// Dense-rotation query preparation, split planning and the C-ABI entry of
+// attention.  The attention work itself is the fused kernel of tq_attn_impl.h.
+#include <algorithm>
+
+#include "tq_attention.h"
+
+namespace tq {
+
+// ------------------------------------------------------------------ qprep ---
+// Dense rotation only: one block per query row (b, h, l), D threads.
+//   q_s = round_qdtype(q * scale_q)     (MLX weak-scalar multiply, :5802)
+//   q_rot = q_s @ R_K^T                 (turboquant_cache.py:4144)
+// Doing this once per row (instead of once per workgroup) keeps the D x D
+// matrix from being re-read by every split.
+template <int QDT>
+__global__ __launch_bounds__(256) void qprep_kernel(AttnParams p) {
+  __shared__ float y[256];
+  const int64_t row = blockIdx.x;  // (b*Hq + h)*L + l
+  const int l = static_cast<int>(row % p.L);
+  const int64_t bh = row / p.L;
+  const int h = static_cast<int>(bh % p.Hq);
+  const int b = static_cast<int>(bh / p.Hq);
+  const int i = threadIdx.x;
+  const int D = p.D;
+  const float qv = load_elem<QDT>(p.q, b * p.q_sb + h * p.q_sh + l * p.q_sl + i);
+  y[i] = round_to<QDT>(qv * p.scale_q);
+  __syncthreads();
+  const float* Rrow = p.krot + static_cast<int64_t>(i) * D;  // y_i = sum_j q_j R[i][j]
+  float acc = 0.f;
+  for (int j = 0; j < D; ++j) acc = fmaf(y[j], Rrow[j], acc);
+  p.qrot[row * D + i] = acc;
+}
+
+// ------------------------------------------------------------- planning ---
+SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T) {
+  SplitPlan sp{};
+  const int R = Hq / Hkv;
+  const int rows = R * L;
+  sp.nq = rows >= 4 ? 4 : (rows >= 2 ? 2 : 1);
+  sp.n_rg = (rows + sp.nq - 1) / sp.nq;
+  const int64_t base = static_cast<int64_t>(B) * Hkv * sp.n_rg;
+  const int64_t target = 4LL * device_cu_count();
+  int64_t ns = base > 0 ? (target + base - 1) / base : 1;
+  const int64_t max_by_tokens = std::max<int64_t>(1, (T + 63) / 64);
+  ns = std::max<int64_t>(1, std::min(ns, max_by_tokens));
+  int64_t chunk = (T + ns - 1) / ns;
+  chunk = std::max<int64_t>(64, (chunk + 63) / 64 * 64);
+  chunk = std::min<int64_t>(chunk, kMaxChunk);
+  sp.chunk = static_cast<int>(chunk);
+  sp.n_splits = static_cast<int>(std::max<int64_t>(1, (T + chunk - 1) / chunk));
+  return sp;
+}
+
+static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Layout: [counters kCounterBytes][q_rot rows*D][partial o rows*splits*D][partial (m,l)].
+int64_t workspace_bytes(const SplitPlan& sp, int B, int Hq, int Hkv, int L, int D) {
+  (void)Hkv;
+  const int64_t rows = static_cast<int64_t>(B) * Hq * L;
+  return kCounterBytes + align256(rows * D * 4) + align256(rows * sp.n_splits * D * 4) +
+         align256(rows * sp.n_splits * 2 * 4);
+}
+
+size_t attn_lds_bytes(const SplitPlan& sp, int D) {
+  const size_t w = static_cast<size_t>(sp.chunk) * sp.nq;
+  const size_t o = static_cast<size_t>(kAttnWaves) * sp.nq * D;
+  const size_t m = static_cast<size_t>(sp.n_splits) * sp.nq;
+  return std::max(w, std::max(o, m)) * sizeof(float);
+}
+
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
+                                               int64_t max_tokens) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || dim <= 0 || max_tokens < 0 || Hq % Hkv)
+    return 0;
+  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, std::max<int64_t>(max_tokens, 1));
+  return workspace_bytes(sp, B, Hq, Hkv, L, dim);
+}
+
+extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                            int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l,
+                            float scale, int kv_kind, int kv_dtype, const void* k,
+                            const void* k_norms, const void* v, const void* v_norms,
+                            int norm_dtype, int k_bits, int v_bits, const float* k_codebook,
+                            const float* v_codebook, int rot_kind, const float* k_rot,
+                            const float* v_rot, int64_t capacity, int64_t max_tokens,
+                            const int32_t* seq_lens, int causal, void* out, void* workspace,
+                            int64_t workspace_bytes_given, void* stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || L < 1 || Hq % Hkv)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bad heads/L (Hq %d, Hkv %d, L %d)", Hq, Hkv, L);
+  if (dim != 64 && dim != 128 && dim != 256)
+    return fail(TQ_ERR_UNSUPPORTED, "attention: dim %d not in {64, 128, 256}", dim);
+  if (q_dtype != TQ_DTYPE_F32 && q_dtype != TQ_DTYPE_F16 && q_dtype != TQ_DTYPE_BF16)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: q_dtype %d", q_dtype);
+  if (max_tokens < 0 || max_tokens > capacity)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: max_tokens %lld > capacity %lld",
+                (long long)max_tokens, (long long)capacity);
+  if (kv_kind == TQ_KV_PACKED) {
+    if (k_bits < 1 || k_bits > 4 || v_bits < 1 || v_bits > 4)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bits k=%d v=%d not in 1..4", k_bits, v_bits);
+    if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: norm_dtype %d", norm_dtype);
+    if (rot_kind != TQ_ROT_HADAMARD && rot_kind != TQ_ROT_DENSE)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: rot_kind %d", rot_kind);
+    if (!k_codebook || !v_codebook || !k_rot || !v_rot)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null codec pointer");
+    if (max_tokens > 0 && (!k_norms || !v_norms))
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null norms pointer");
+  } else if (kv_kind == TQ_KV_PLAIN) {
+    if (kv_dtype != TQ_DTYPE_F16 && kv_dtype != TQ_DTYPE_BF16)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: plain kv_dtype %d", kv_dtype);
+  } else {
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: kv_kind %d", kv_kind);
+  }
+  if (B == 0) return TQ_OK;
+  if (!q || !out || !workspace) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null pointer");
+  if (max_tokens > 0 && (!k || !v)) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null cache pointer");
+  const int64_t T = std::max<int64_t>(max_tokens, 1);
+  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, T);
+  if (static_cast<int64_t>(B) * Hkv * sp.n_rg > kMaxGroups)
+    return fail(TQ_ERR_UNSUPPORTED, "attention: %lld (batch, kv head, row group) groups > %d",
+                (long long)B * Hkv * sp.n_rg, kMaxGroups);
+  if (sp.n_splits > kMaxSplits)
+    return fail(TQ_ERR_UNSUPPORTED, "attention: %lld tokens exceed %d splits of %d",
+                (long long)T, kMaxSplits, sp.chunk);
+  const int64_t need = workspace_bytes(sp, B, Hq, Hkv, L, dim);
+  if (workspace_bytes_given < need)
+    return fail(TQ_ERR_WORKSPACE, "attention: workspace %lld < %lld bytes",
+                (long long)workspace_bytes_given, (long long)need);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: workspace must be 256-byte aligned");
+
+  AttnParams p{};
+  p.q = q;
+  p.q_sb = q_stride_b;
+  p.q_sh = q_stride_h;
+  p.q_sl = q_stride_l;
+  p.q_dtype = q_dtype;
+  p.scale_q = host_round_to(q_dtype, scale);
+  p.k = k;
+  p.kn = k_norms;
+  p.v = v;
+  p.vn = v_norms;
+  p.norm_dtype = norm_dtype;
+  p.kcb = k_codebook;
+  p.vcb = v_codebook;
+  p.rot_kind = rot_kind;
+  p.krot = k_rot;
+  p.vrot = v_rot;
+  p.seq_lens = seq_lens;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.L = L;
+  p.R = Hq / Hkv;
+  p.D = dim;
+  p.cap = capacity;
+  p.T = max_tokens;
+  p.causal = causal ? 1 : 0;
+  p.n_splits = sp.n_splits;
+  p.chunk = sp.chunk;
+  p.n_rg = sp.n_rg;
+  p.nq = sp.nq;
+  const int64_t rows = static_cast<int64_t>(B) * Hq * L;
+  char* ws = static_cast<char*>(workspace);
+  p.counters = reinterpret_cast<uint32_t*>(ws);
+  ws += kCounterBytes;
+  p.qrot = reinterpret_cast<float*>(ws);
+  ws += (rows * dim * 4 + 255) / 256 * 256;
+  p.po = reinterpret_cast<float*>(ws);
+  ws += (rows * sp.n_splits * dim * 4 + 255) / 256 * 256;
+  p.pml = reinterpret_cast<float*>(ws);
+  p.out = out;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  p.rscale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
+  int rc = TQ_OK;
+  if (kv_kind == TQ_KV_PACKED && rot_kind == TQ_ROT_DENSE) {
+    const dim3 rgrid(static_cast<unsigned>(rows));
+    switch (q_dtype) {
+      case TQ_DTYPE_F32: hipLaunchKernelGGL(qprep_kernel<TQ_DTYPE_F32>, rgrid, dim3(dim), 0, st, p); break;
+      case TQ_DTYPE_F16: hipLaunchKernelGGL(qprep_kernel<TQ_DTYPE_F16>, rgrid, dim3(dim), 0, st, p); break;
+      default: hipLaunchKernelGGL(qprep_kernel<TQ_DTYPE_BF16>, rgrid, dim3(dim), 0, st, p); break;
+    }
+    rc = check_launch("qprep_kernel");
+    if (rc) return rc;
+  }
+  p.T = max_tokens;
+  switch (dim) {
+    case 64: return launch_partial_d64(p, kv_kind, kv_dtype, k_bits, v_bits, st);
+    case 128: return launch_partial_d128(p, kv_kind, kv_dtype, k_bits, v_bits, st);
+    default: return launch_partial_d256(p, kv_kind, kv_dtype, k_bits, v_bits, st);
+  }
+}

@@ -1,0 +1,281 @@
+"""torch-facing wrappers over the C ABI (device pointers + the current stream).
+
+Every function here enqueues HIP kernels from libkaplumba_tq.so on torch's
+current stream for the tensor's device.  Tensors must live on a ROCm device;
+there is no CPU path.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from . import codebook as cbmod
+
+ROTATIONS = {"hadamard": _lib.TQ_ROT_HADAMARD, "dense": _lib.TQ_ROT_DENSE}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise ValueError("TurboQuant kernels need ROCm device tensors "
+                             f"(got {getattr(t, 'device', type(t))}); there is no CPU path")
+
+
+@dataclass
+class Codec:
+    """One quantizer: dim, bits, seed, rotation kind and codebook kind.
+
+    Mirrors ``_TurboQuantMSECodec.__init__`` (turboquant_cache.py:4122-4139):
+    Hadamard rotation with signs for power-of-two dims, a dense QR rotation
+    otherwise (or when asked for), the Lloyd-Max codebook and its midpoints.
+    """
+
+    dim: int
+    bits: int
+    seed: int
+    rotation: str = "auto"
+    codebook_kind: str = "beta"
+    _dev: Dict[str, Dict[str, torch.Tensor]] = field(default_factory=dict, repr=False)
+
+    def __post_init__(self) -> None:
+        pow2 = self.dim > 0 and (self.dim & (self.dim - 1)) == 0
+        if self.rotation == "auto":
+            self.rotation = "hadamard" if pow2 else "dense"
+        if self.rotation not in ROTATIONS:
+            raise ValueError(f"rotation must be 'auto', 'hadamard' or 'dense', got {self.rotation!r}")
+        if self.rotation == "hadamard" and not pow2:
+            raise ValueError(f"Hadamard rotation needs a power-of-two head dim, got {self.dim}")
+        self.use_rht = self.rotation == "hadamard"
+        self.codebook = cbmod.codebook(self.dim, self.bits, self.codebook_kind)
+        self.midpoints = cbmod.midpoints(self.codebook)
+        self.packed_width = cbmod.packed_width(self.dim, self.bits)
+
+    @property
+    def rot_kind(self) -> int:
+        return ROTATIONS[self.rotation]
+
+    @property
+    def rot_host(self) -> np.ndarray:
+        if self.use_rht:
+            return cbmod.rht_sign_vector(self.dim, self.seed)
+        return cbmod.rotation_matrix(self.dim, self.seed)
+
+    def device_tensors(self, device: torch.device) -> Dict[str, torch.Tensor]:
+        key = str(device)
+        d = self._dev.get(key)
+        if d is None:
+            d = {
+                "rot": torch.from_numpy(np.ascontiguousarray(self.rot_host)).to(device),
+                "codebook": torch.from_numpy(self.codebook.copy()).to(device),
+                "midpoints": torch.from_numpy(
+                    self.midpoints.copy() if self.midpoints.size else np.zeros(1, np.float32)).to(device),
+            }
+            self._dev[key] = d
+        return d
+
+
+def append_quantize(x: torch.Tensor, codec: Codec, packed: torch.Tensor, norms: torch.Tensor,
+                    offset: int) -> None:
+    """Quantize x (B, H, L, D) into rows offset..offset+L of the capacity buffers.
+
+    packed: (B, H, cap, PW) uint32 contiguous; norms: (B, H, cap) f32/f16 contiguous.
+    """
+    _require_device(x, packed, norms)
+    B, H, L, D = x.shape
+    if D != codec.dim:
+        raise ValueError(f"head dim {D} != codec dim {codec.dim}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    if not (packed.is_contiguous() and norms.is_contiguous()):
+        raise ValueError("cache buffers must be contiguous")
+    cap = packed.shape[2]
+    if packed.shape != (B, H, cap, codec.packed_width) or norms.shape != (B, H, cap):
+        raise ValueError(f"buffer shapes {tuple(packed.shape)}/{tuple(norms.shape)} "
+                         f"do not match ({B}, {H}, cap, {codec.packed_width})")
+    es = x.element_size()
+    if x.data_ptr() % 16 or any((s * es) % 16 for s in x.stride()[:3]):
+        x = x.contiguous()
+    dt = codec.device_tensors(x.device)
+    lib = _lib.load()
+    rc = lib.tq_append_quantize(
+        x.data_ptr(), _lib.torch_dtype_code(x.dtype), B, H, L, D,
+        x.stride(0), x.stride(1), x.stride(2),
+        codec.bits, codec.rot_kind, dt["rot"].data_ptr(), dt["midpoints"].data_ptr(),
+        packed.data_ptr(), norms.data_ptr(), _lib.torch_dtype_code(norms.dtype),
+        cap, offset, _stream(x))
+    _lib.check(rc, "tq_append_quantize")
+
+
+def append_plain(x: torch.Tensor, dst: torch.Tensor, offset: int) -> None:
+    """Copy x (B, H, L, D) into rows offset.. of dst (B, H, cap, D) (fp16/bf16)."""
+    _require_device(x, dst)
+    B, H, L, D = x.shape
+    if x.dtype != dst.dtype:
+        x = x.to(dst.dtype)
+    if x.stride(-1) != 1 or x.data_ptr() % 16 or any((s * 2) % 16 for s in x.stride()[:3]):
+        x = x.contiguous()
+    if not dst.is_contiguous() or dst.shape[:2] != (B, H) or dst.shape[3] != D:
+        raise ValueError("plain buffer must be contiguous (B, H, cap, D)")
+    rc = _lib.load().tq_append_plain(
+        x.data_ptr(), _lib.torch_dtype_code(x.dtype), B, H, L, D,
+        x.stride(0), x.stride(1), x.stride(2), dst.data_ptr(), dst.shape[2], offset, _stream(x))
+    _lib.check(rc, "tq_append_plain")
+
+
+def _capacity_of(norms: torch.Tensor, indices: torch.Tensor, pw: int) -> int:
+    """Token capacity of the contiguous (B, H, cap[, PW]) buffer a state view slices.
+
+    State views returned by the cache are ``buf[..., :T]`` slices, so the
+    capacity is recovered from the strides; a fresh contiguous state has
+    capacity T.
+    """
+    B, H, T = norms.shape
+    if H > 1:
+        cap = norms.stride(1)
+    elif B > 1:
+        cap = norms.stride(0)
+    else:
+        cap = max(T, 1)
+    ok = indices.shape[:3] == norms.shape and indices.shape[3] == pw
+    ok = ok and (T <= 1 or (norms.stride(2) == 1 and indices.stride(2) == pw))
+    ok = ok and indices.stride(3) == 1 and cap >= T
+    if H > 1:
+        ok = ok and indices.stride(1) == cap * pw
+    if B > 1:
+        ok = ok and norms.stride(0) == H * cap and indices.stride(0) == H * cap * pw
+    if not ok:
+        raise ValueError("state views must slice contiguous (B, H, cap) norms and "
+                         f"(B, H, cap, {pw}) index buffers")
+    return cap
+
+
+def dequantize(indices: torch.Tensor, norms: torch.Tensor, codec: Codec) -> torch.Tensor:
+    """f32 (B, H, T, D) reconstruction n * R^-1(codebook[idx])."""
+    _require_device(indices, norms)
+    B, H, T = norms.shape
+    out = torch.empty((B, H, T, codec.dim), dtype=torch.float32, device=norms.device)
+    if B * H * T == 0:
+        return out
+    cap = _capacity_of(norms, indices, codec.packed_width)
+    dt = codec.device_tensors(norms.device)
+    rc = _lib.load().tq_dequantize(
+        indices.data_ptr(), norms.data_ptr(), _lib.torch_dtype_code(norms.dtype),
+        B, H, T, codec.dim, codec.bits, cap, dt["codebook"].data_ptr(), codec.rot_kind,
+        dt["rot"].data_ptr(), out.data_ptr(), _stream(norms))
+    _lib.check(rc, "tq_dequantize")
+    return out
+
+
+_WORKSPACES: Dict[tuple, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Persistent attention workspace per (device, stream).
+
+    The kernel keeps merge counters at the head of the workspace and needs
+    them zero on entry; it resets them before returning, so a buffer zeroed
+    once at allocation stays valid for every later call on that stream.
+    """
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.Tensor,
+                     v_norms: torch.Tensor, v_idx: torch.Tensor, key_codec: Codec,
+                     value_codec: Codec, scale: float, causal: bool,
+                     seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention straight from packed K/V state views (B, Hkv, T[, PW])."""
+    _require_device(queries, k_norms, k_idx, v_norms, v_idx)
+    B, Hq, L, D = queries.shape
+    Hkv, T = k_norms.shape[1], k_norms.shape[2]
+    if key_codec.dim != D or value_codec.dim != D:
+        raise NotImplementedError(
+            f"attention with key dim {key_codec.dim} / value dim {value_codec.dim} "
+            f"and query dim {D}: only equal K/V head dims are built")
+    if key_codec.rotation != value_codec.rotation:
+        raise NotImplementedError("K and V codecs must use the same rotation kind")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} kv heads")
+    if queries.stride(-1) != 1:
+        queries = queries.contiguous()
+    cap = _capacity_of(k_norms, k_idx, key_codec.packed_width)
+    vcap = _capacity_of(v_norms, v_idx, value_codec.packed_width)
+    if vcap != cap:
+        raise ValueError("key and value buffers must share a capacity")
+    if k_norms.dtype != v_norms.dtype:
+        raise ValueError("key and value norms must share a dtype")
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(device=queries.device, dtype=torch.int32).contiguous()
+    out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
+    lib = _lib.load()
+    wsb = lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T)
+    ws = _workspace(queries.device, wsb)
+    kt = key_codec.device_tensors(queries.device)
+    vt = value_codec.device_tensors(queries.device)
+    rc = lib.tq_attention(
+        queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
+        queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
+        _lib.TQ_KV_PACKED, 0,
+        k_idx.data_ptr(), k_norms.data_ptr(), v_idx.data_ptr(), v_norms.data_ptr(),
+        _lib.torch_dtype_code(k_norms.dtype), key_codec.bits, value_codec.bits,
+        kt["codebook"].data_ptr(), vt["codebook"].data_ptr(), key_codec.rot_kind,
+        kt["rot"].data_ptr(), vt["rot"].data_ptr(), cap, T,
+        seq_lens.data_ptr() if seq_lens is not None else None, 1 if causal else 0,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
+    _lib.check(rc, "tq_attention")
+    return out
+
+
+def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                    scale: float, causal: bool,
+                    seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention over unquantized fp16/bf16 K/V views (B, Hkv, T, D) of (B, Hkv, cap, D)."""
+    _require_device(queries, keys, values)
+    B, Hq, L, D = queries.shape
+    Hkv, T = keys.shape[1], keys.shape[2]
+    if keys.dtype != values.dtype or keys.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("plain K/V must both be float16 or bfloat16")
+    if keys.shape[-1] != D or values.shape[-1] != D:
+        raise NotImplementedError("only equal query/key/value head dims are built")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} kv heads")
+    for t in (keys, values):
+        if t.stride(3) != 1 or t.stride(2) != D:
+            raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
+    if Hkv > 1:
+        cap = keys.stride(1) // D
+    elif B > 1:
+        cap = keys.stride(0) // D
+    else:
+        cap = max(T, 1)
+    if keys.stride() != values.stride() or (B > 1 and keys.stride(0) != Hkv * cap * D):
+        raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
+    if queries.stride(-1) != 1:
+        queries = queries.contiguous()
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(device=queries.device, dtype=torch.int32).contiguous()
+    out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
+    lib = _lib.load()
+    wsb = lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T)
+    ws = _workspace(queries.device, wsb)
+    rc = lib.tq_attention(
+        queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
+        queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
+        _lib.TQ_KV_PLAIN, _lib.torch_dtype_code(keys.dtype),
+        keys.data_ptr(), None, values.data_ptr(), None, 0, 0, 0, None, None, 0, None, None,
+        cap, T, seq_lens.data_ptr() if seq_lens is not None else None, 1 if causal else 0,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
+    _lib.check(rc, "tq_attention(plain)")
+    return out

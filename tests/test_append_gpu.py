@@ -1,0 +1,150 @@
+"""GPU parity of the append-time quantizer (C ABI tq_append_quantize) vs the oracle.
+
+Bar: packed index words and norms bit-exact.  Covers every Hadamard dim
+(32..512), bits 1..4, f16/bf16/f32 inputs, f32/f16 norms, strided inputs,
+writes at an offset inside a capacity buffer, zero / tiny / large vectors and
+the full config-0 layer (K and V f16 [1, 8, 4096, 128], 3-bit).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+from kaplumba_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _buffers(B, H, cap, codec, norm_dtype, device):
+    packed = torch.zeros((B, H, cap, codec.packed_width), dtype=torch.uint32, device=device)
+    norms = torch.zeros((B, H, cap), dtype=norm_dtype, device=device)
+    return packed, norms
+
+
+def _np_u32(t):
+    return t.cpu().numpy().astype(np.uint32)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_fixture_vectors_bit_exact(golden, device, d, bits):
+    q = golden["quantize"]
+    x = torch.from_numpy(q[f"x_{d}"].reshape(1, 2, 24, d)).to(device)
+    codec = ops.Codec(d, bits, 0)
+    packed, norms = _buffers(1, 2, 30, codec, torch.float32, device)
+    ops.append_quantize(x, codec, packed, norms, offset=3)
+    got_p = _np_u32(packed)
+    got_n = norms.cpu().numpy()
+    want_p = q[f"packed_{d}_{bits}"].reshape(1, 2, 24, -1)
+    want_n = q[f"norms_{d}_{bits}"].reshape(1, 2, 24)
+    assert np.array_equal(got_p[:, :, 3:27], want_p)
+    assert np.array_equal(got_n[:, :, 3:27], want_n)
+    assert not got_p[:, :, :3].any() and not got_p[:, :, 27:].any()
+    assert not got_n[:, :, :3].any() and not got_n[:, :, 27:].any()
+
+
+def test_fixture_f32_input_f16_norms_seed1(golden, device):
+    q = golden["quantize"]
+    x = torch.from_numpy(q["x32_128"].reshape(1, 1, 40, 128)).to(device)
+    codec = ops.Codec(128, 3, 1)
+    packed, norms = _buffers(1, 1, 40, codec, torch.float16, device)
+    ops.append_quantize(x, codec, packed, norms, 0)
+    assert np.array_equal(_np_u32(packed)[0, 0], q["packed32_128_3_seed1"])
+    assert np.array_equal(norms.cpu().numpy()[0, 0], q["norms16_128_3_seed1"])
+
+
+def test_fixture_bf16_input_gaussian_codebook(golden, device):
+    q = golden["quantize"]
+    bits16 = torch.from_numpy(q["xbf16_bits_128"].astype(np.int16))
+    x = bits16.view(torch.bfloat16).reshape(1, 1, 40, 128).to(device)
+    codec = ops.Codec(128, 4, 0, codebook_kind="gaussian")
+    packed, norms = _buffers(1, 1, 40, codec, torch.float32, device)
+    ops.append_quantize(x, codec, packed, norms, 0)
+    assert np.array_equal(_np_u32(packed)[0, 0], q["packedbf16_128_4_gauss"])
+    assert np.array_equal(norms.cpu().numpy()[0, 0], q["normsbf16_128_4_gauss"])
+
+
+def _synth(rng, shape, dtype):
+    B, H, L, D = shape
+    s = np.exp(rng.normal(0, 0.5, size=(1, H, 1, D)))
+    return (rng.standard_normal(shape) * s).astype(np.float32), dtype
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+@pytest.mark.parametrize("norm_dtype", [torch.float32, torch.float16])
+def test_random_batches_strided_input(device, dtype, bits, norm_dtype):
+    rng = np.random.default_rng(bits * 10 + (dtype == torch.bfloat16))
+    B, H, L, D = 2, 8, 37, 128
+    x32, _ = _synth(rng, (B, H, L, D), dtype)
+    # model layout (B, L, H, D) transposed to (B, H, L, D): non-contiguous view
+    xt = torch.from_numpy(x32).to(dtype).transpose(1, 2).contiguous().transpose(1, 2).to(device)
+    assert not xt.is_contiguous()
+    xin = xt.float().cpu().numpy()
+    codec = ops.Codec(D, bits, 5)
+    packed, norms = _buffers(B, H, 64, codec, norm_dtype, device)
+    ops.append_quantize(xt, codec, packed, norms, offset=11)
+    nd = "float16" if norm_dtype == torch.float16 else "float32"
+    wp, wn = O.quantize_rht(xin, bits, O.rht_signs(D, 5), O.beta_codebook(D, bits), nd)
+    assert np.array_equal(_np_u32(packed)[:, :, 11:48], wp)
+    assert np.array_equal(norms.float().cpu().numpy()[:, :, 11:48], wn)
+
+
+def test_edge_vectors(device):
+    D = 128
+    x = np.zeros((1, 1, 6, D), np.float32)
+    x[0, 0, 1] = 1e-30                           # subnormal-scale input, norm ~1e-29
+    x[0, 0, 2, 5] = 3.0                          # one-hot
+    x[0, 0, 3] = 60000.0                         # near f16 max
+    x[0, 0, 4] = np.linspace(-1, 1, D)
+    x[0, 0, 5, ::2] = -2.5
+    for bits in (1, 2, 3, 4):
+        codec = ops.Codec(D, bits, 0)
+        packed, norms = _buffers(1, 1, 6, codec, torch.float32, device)
+        ops.append_quantize(torch.from_numpy(x).to(device), codec, packed, norms, 0)
+        wp, wn = O.quantize_rht(x, bits, O.rht_signs(D, 0), O.beta_codebook(D, bits))
+        assert np.array_equal(_np_u32(packed), wp), bits
+        assert np.array_equal(norms.cpu().numpy(), wn), bits
+
+
+def test_config0_full_layer_bit_exact(device):
+    """K and V f16 [1, 8, 4096, 128], per-channel log-normal scales, 3-bit."""
+    rs, rk, rv = (np.random.default_rng(s) for s in (1000, 1001, 1002))
+    scale = np.exp(rs.normal(0.0, 0.5, size=(1, 8, 1, 128)))
+    k = (rk.standard_normal((1, 8, 4096, 128)) * scale).astype(np.float16)
+    v = (rv.standard_normal((1, 8, 4096, 128)) * scale).astype(np.float16)
+    for x, seed in ((k, 0), (v, 1)):
+        codec = ops.Codec(128, 3, seed)
+        packed, norms = _buffers(1, 8, 4096, codec, torch.float32, device)
+        ops.append_quantize(torch.from_numpy(x).to(device), codec, packed, norms, 0)
+        wp, wn = O.quantize_rht(x, 3, O.rht_signs(128, seed), O.beta_codebook(128, 3))
+        gp = _np_u32(packed)
+        mism = int((gp != wp).sum())
+        assert mism == 0, f"{mism} packed words differ"
+        assert np.array_equal(norms.cpu().numpy(), wn)
+        # reconstruction quality (reference test: cosine > 0.85 at 3 bits)
+        deq = ops.dequantize(packed, norms, codec).cpu().numpy().astype(np.float64)
+        xf = x.astype(np.float64)
+        cos = (deq * xf).sum(-1) / (np.linalg.norm(deq, axis=-1) * np.linalg.norm(xf, axis=-1))
+        assert cos.mean() > 0.97
+
+
+@pytest.mark.parametrize("d,bits", [(64, 2), (128, 3), (256, 4)])
+def test_dequantize_matches_oracle(device, d, bits):
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal((2, 3, 9, d)).astype(np.float32)
+    codec = ops.Codec(d, bits, 0)
+    packed, norms = _buffers(2, 3, 16, codec, torch.float32, device)
+    ops.append_quantize(torch.from_numpy(x).to(device), codec, packed, norms, 0)
+    got = ops.dequantize(packed[:, :, :9], norms[:, :, :9], codec).cpu().numpy()
+    want = O.dequantize(_np_u32(packed[:, :, :9]), norms[:, :, :9].cpu().numpy(), bits, d,
+                        O.beta_codebook(d, bits), "hadamard", O.rht_signs(d, 0))
+    np.testing.assert_allclose(got, want, atol=1e-5)
+
+
+def test_plain_append_copies_rows(device):
+    x = torch.randn(2, 4, 5, 128, dtype=torch.float16, device=device)
+    dst = torch.zeros(2, 4, 16, 128, dtype=torch.float16, device=device)
+    ops.append_plain(x.transpose(1, 2).contiguous().transpose(1, 2), dst, 7)
+    assert torch.equal(dst[:, :, 7:12], x)
+    assert not dst[:, :, :7].any() and not dst[:, :, 12:].any()

@@ -1,0 +1,191 @@
+"""GPU parity of decode / verify attention (C ABI tq_attention) vs the oracle.
+
+Bar: outputs within 2e-3 max-abs and 1e-3 mean-rel of
+the float64 TurboQuant attention, after both are rounded to the query dtype;
+mean-rel is mean(|got - want|) / mean(|want|).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+from kaplumba_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-3
+MEAN_REL = 1e-3
+QDT = {0: "f32", 1: "f16", 2: "bf16"}
+TORCH_QDT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def assert_close(got: torch.Tensor, want64: np.ndarray, qdt: str, label=""):
+    g = got.float().cpu().numpy().astype(np.float64)
+    w = O.round_to_dtype(want64.astype(np.float32), qdt).astype(np.float64)
+    err = np.abs(g - w)
+    mean_rel = err.mean() / max(np.abs(w).mean(), 1e-30)
+    print(f"[{label}] max_abs={err.max():.3e} mean_rel={mean_rel:.3e}", flush=True)
+    assert err.max() <= MAX_ABS, (label, err.max())
+    assert mean_rel <= MEAN_REL, (label, mean_rel)
+
+
+def to_buffers(kp, kn, vp, vn, device, extra=7, norm_dtype=torch.float32):
+    """Place (B, H, T, PW)/(B, H, T) arrays in larger capacity buffers; return views."""
+    B, H, T = kn.shape
+    cap = T + extra
+    out = []
+    for p, n in ((kp, kn), (vp, vn)):
+        pb = torch.zeros((B, H, cap, p.shape[-1]), dtype=torch.uint32, device=device)
+        nb = torch.zeros((B, H, cap), dtype=norm_dtype, device=device)
+        pb[:, :, :T] = torch.from_numpy(p.astype(np.uint32)).to(device)
+        nb[:, :, :T] = torch.from_numpy(np.asarray(n, np.float32)).to(device).to(norm_dtype)
+        out += [nb[:, :, :T], pb[:, :, :T]]
+    return out  # k_norms, k_idx, v_norms, v_idx
+
+
+def q_tensor(q_np, qdt, device):
+    return torch.from_numpy(q_np.astype(np.float32)).to(TORCH_QDT[qdt]).to(device)
+
+
+@pytest.mark.parametrize("case", ["decode_d128_k3v3", "verify_d128_k2v1", "ragged_d256_k4v2_dense",
+                                  "decode_d64_k4v4_f32q"])
+def test_golden_cases(golden, device, case):
+    a = golden["attention"]
+    B, Hq, Hkv, L, T, d, kb, vb, dense, causal = (int(v) for v in a[f"{case}/meta"])
+    qdt = QDT[int(a[f"{case}/qdtype"][0])]
+    rot = "dense" if dense else "hadamard"
+    kn, ki, vn, vi = to_buffers(a[f"{case}/k_packed"], a[f"{case}/k_norms"], a[f"{case}/v_packed"],
+                                a[f"{case}/v_norms"], device)
+    kc, vc = ops.Codec(d, kb, 0, rot), ops.Codec(d, vb, 1, rot)
+    lengths = torch.from_numpy(a[f"{case}/lengths"]).to(device)
+    out = ops.attention_packed(q_tensor(a[f"{case}/q"], qdt, device), kn, ki, vn, vi, kc, vc,
+                               1.0 / math.sqrt(d), bool(causal), seq_lens=lengths)
+    assert_close(out, a[f"{case}/expected"].astype(np.float64), qdt, case)
+
+
+def test_golden_plain_f16(golden, device):
+    a = golden["attention"]
+    q = q_tensor(a["plain_f16/q"], "f16", device)
+    kb = torch.zeros((1, 2, 230, 128), dtype=torch.float16, device=device)
+    vb = torch.zeros_like(kb)
+    kb[:, :, :200] = torch.from_numpy(a["plain_f16/k"]).to(device)
+    vb[:, :, :200] = torch.from_numpy(a["plain_f16/v"]).to(device)
+    out = ops.attention_plain(q, kb[:, :, :200], vb[:, :, :200], 1 / math.sqrt(128), True)
+    assert_close(out, a["plain_f16/expected"].astype(np.float64), "f16", "plain_f16")
+
+
+def build_case(seed, B, Hq, Hkv, L, T, d, kb, vb, rot="hadamard", qdt="bf16", norm="float32"):
+    rng = np.random.default_rng(seed)
+    s = np.exp(rng.normal(0, 0.5, size=(1, Hkv, 1, d)))
+    k = (rng.standard_normal((B, Hkv, T, d)) * s).astype(np.float16).astype(np.float32)
+    v = (rng.standard_normal((B, Hkv, T, d)) * s).astype(np.float16).astype(np.float32)
+    if rot == "hadamard":
+        kr, vr = O.rht_signs(d, 0), O.rht_signs(d, 1)
+        kp, kn = O.quantize_rht(k, kb, kr, O.beta_codebook(d, kb), norm)
+        vp, vn = O.quantize_rht(v, vb, vr, O.beta_codebook(d, vb), norm)
+    else:
+        kr, vr = O.rotation_matrix(d, 0), O.rotation_matrix(d, 1)
+        kp, kn, _ = O.quantize_dense(k, kb, kr, O.beta_codebook(d, kb), norm)
+        vp, vn, _ = O.quantize_dense(v, vb, vr, O.beta_codebook(d, vb), norm)
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, d)).astype(np.float32), qdt)
+    return q, kp, kn, vp, vn, kr, vr
+
+
+def run_case(device, seed, B, Hq, Hkv, L, T, d, kb, vb, rot="hadamard", qdt="bf16", causal=None,
+             lengths=None, norm="float32"):
+    causal = (L > 1) if causal is None else causal
+    q, kp, kn, vp, vn, kr, vr = build_case(seed, B, Hq, Hkv, L, T, d, kb, vb, rot, qdt, norm)
+    want = O.attention(q, kp, kn, vp, vn, k_bits=kb, v_bits=vb, k_codebook=O.beta_codebook(d, kb),
+                       v_codebook=O.beta_codebook(d, vb), rot_kind=rot, k_rot=kr, v_rot=vr,
+                       scale=1 / math.sqrt(d), q_dtype=qdt, causal=causal, lengths=lengths)
+    nd = torch.float16 if norm == "float16" else torch.float32
+    kn_t, ki, vn_t, vi = to_buffers(kp, kn, vp, vn, device, norm_dtype=nd)
+    sl = torch.tensor(lengths, dtype=torch.int32, device=device) if lengths is not None else None
+    out = ops.attention_packed(q_tensor(q, qdt, device), kn_t, ki, vn_t, vi,
+                               ops.Codec(d, kb, 0, rot), ops.Codec(d, vb, 1, rot),
+                               1 / math.sqrt(d), causal, seq_lens=sl)
+    label = f"B{B} Hq{Hq} Hkv{Hkv} L{L} T{T} d{d} k{kb}v{vb} {rot} {qdt}"
+    assert_close(out, want, qdt, label)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("kb,vb", [(1, 1), (2, 2), (3, 3), (4, 4), (4, 2), (2, 1), (3, 4), (1, 3)])
+def test_decode_bits_and_dims(device, d, kb, vb):
+    run_case(device, 100 + d + 10 * kb + vb, 1, 8, 2, 1, 777, d, kb, vb)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (8, 1), (24, 8)])
+@pytest.mark.parametrize("L", [1, 2, 4])
+def test_gqa_groups_and_verify_rows(device, Hq, Hkv, L):
+    run_case(device, Hq * 7 + Hkv + L, 1, Hq, Hkv, L, 1500, 128, 3, 3)
+
+
+@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 2048, 5000])
+def test_token_counts(device, T):
+    run_case(device, T, 1, 8, 2, 1, T, 128, 3, 3)
+    run_case(device, T + 1, 1, 8, 2, 4, max(T, 4), 128, 2, 1)
+
+
+@pytest.mark.parametrize("qdt", ["f32", "f16", "bf16"])
+def test_query_dtypes_and_f16_norms(device, qdt):
+    run_case(device, 5, 2, 8, 2, 1, 600, 128, 3, 3, qdt=qdt, norm="float16")
+
+
+def test_ragged_batch_dense_d256(device):
+    """Config-2 shape at reduced size: ragged lengths, d=256, K4/V2, dense rotation."""
+    lengths = [300, 1, 1700, 0, 999]
+    run_case(device, 77, 5, 16, 8, 1, 1700, 256, 4, 2, rot="dense", lengths=lengths)
+
+
+def test_ragged_verify_causal(device):
+    run_case(device, 78, 3, 8, 2, 4, 900, 128, 2, 1, lengths=[4, 900, 517], causal=True)
+
+
+def test_empty_cache_gives_zeros(device):
+    q = torch.randn(1, 8, 1, 128, dtype=torch.bfloat16, device=device)
+    kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)
+    kn = torch.zeros((1, 2, 4), device=device)
+    ki = torch.zeros((1, 2, 4, 12), dtype=torch.uint32, device=device)
+    out = ops.attention_packed(q, kn[:, :, :0], ki[:, :, :0], kn[:, :, :0], ki[:, :, :0], kc, vc,
+                               0.1, False)
+    assert out.shape == (1, 8, 1, 128) and not out.float().abs().sum().item()
+
+
+def test_repeated_calls_reuse_workspace_counters(device):
+    """The merge counters must come back to zero: run shapes of different group counts."""
+    for B, Hkv, T in ((1, 2, 300), (3, 8, 5000), (1, 2, 300), (2, 4, 70)):
+        run_case(device, B * 13 + T, B, Hkv * 4, Hkv, 1, T, 128, 3, 3)
+
+
+def test_config1_full_size(device):
+    """Config 1: 32 q heads / 8 kv heads, d=128, 32768 tokens, 3-bit, bf16 query.
+
+    The cache is written by the HIP append kernel (bit-exact vs the oracle)
+    and attention is checked against the float64 oracle at full size.
+    """
+    rs, rk, rv, rq = (np.random.default_rng(s) for s in (1000, 1001, 1002, 1003))
+    T = 32768
+    scale = np.exp(rs.normal(0.0, 0.5, size=(1, 8, 1, 128)))
+    k = (rk.standard_normal((1, 8, T, 128)) * scale).astype(np.float16)
+    v = (rv.standard_normal((1, 8, T, 128)) * scale).astype(np.float16)
+    q = O.round_to_dtype(rq.standard_normal((1, 32, 1, 128)).astype(np.float32), "bf16")
+    kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)
+    bufs = []
+    for x, c in ((k, kc), (v, vc)):
+        pb = torch.zeros((1, 8, T, 12), dtype=torch.uint32, device=device)
+        nb = torch.zeros((1, 8, T), dtype=torch.float32, device=device)
+        ops.append_quantize(torch.from_numpy(x).to(device), c, pb, nb, 0)
+        bufs.append((pb, nb))
+    (kp, kn), (vp, vn) = bufs
+    kp_np, vp_np = kp.cpu().numpy().astype(np.uint32), vp.cpu().numpy().astype(np.uint32)
+    wkp, wkn = O.quantize_rht(k, 3, O.rht_signs(128, 0), O.beta_codebook(128, 3))
+    assert np.array_equal(kp_np, wkp) and np.array_equal(kn.cpu().numpy(), wkn)
+    out = ops.attention_packed(q_tensor(q, "bf16", device), kn, kp, vn, vp, kc, vc,
+                               1 / math.sqrt(128), False)
+    want = O.attention(q, kp_np, kn.cpu().numpy(), vp_np, vn.cpu().numpy(), k_bits=3, v_bits=3,
+                       k_codebook=O.beta_codebook(128, 3), v_codebook=O.beta_codebook(128, 3),
+                       rot_kind="hadamard", k_rot=O.rht_signs(128, 0), v_rot=O.rht_signs(128, 1),
+                       scale=1 / math.sqrt(128), q_dtype="bf16")
+    assert_close(out, want, "bf16", "config1")

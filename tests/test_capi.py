@@ -1,0 +1,95 @@
+"""The C-ABI library loads, exports every declared symbol and validates input (CPU only).
+
+No test here launches a kernel: argument checks run on the host before any
+HIP call, so they are exercised without a GPU.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from kaplumba_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "kaplumba_tq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tq_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_set():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_version_and_packed_width():
+    lib = _lib.load()
+    assert lib.tq_version().startswith(b"kaplumba_tq")
+    assert lib.tq_packed_width(128, 3) == 12
+    assert lib.tq_packed_width(256, 4) == 32
+    assert lib.tq_packed_width(64, 1) == 2
+    assert lib.tq_packed_width(0, 3) == 0
+
+
+def test_workspace_size_is_positive_and_grows():
+    lib = _lib.load()
+    a = lib.tq_attention_workspace_size(1, 32, 8, 1, 128, 32768)
+    b = lib.tq_attention_workspace_size(4, 32, 8, 4, 128, 131072)
+    assert 0 < a < b
+    assert lib.tq_attention_workspace_size(1, 32, 7, 1, 128, 10) == 0  # Hq % Hkv != 0
+
+
+@pytest.mark.parametrize("bits", [0, 5])
+def test_append_rejects_bad_bits_without_touching_the_gpu(bits):
+    lib = _lib.load()
+    rc = lib.tq_append_quantize(None, 1, 1, 1, 1, 128, 128, 128, 128, bits, 0, None, None,
+                                None, None, 0, 16, 0, None)
+    assert rc == _lib.TQ_ERR_INVALID_ARGUMENT
+    assert b"bits" in lib.tq_last_error()
+
+
+def test_append_rejects_capacity_overflow_and_nulls():
+    lib = _lib.load()
+    rc = lib.tq_append_quantize(None, 1, 1, 1, 5, 128, 640, 640, 128, 3, 0, None, None,
+                                None, None, 0, 4, 0, None)
+    assert rc == _lib.TQ_ERR_INVALID_ARGUMENT and b"capacity" in lib.tq_last_error()
+    rc = lib.tq_append_quantize(None, 1, 1, 1, 1, 128, 128, 128, 128, 3, 0, None, None,
+                                None, None, 0, 4, 0, None)
+    assert rc == _lib.TQ_ERR_INVALID_ARGUMENT and b"null" in lib.tq_last_error()
+    # empty append is a no-op success
+    assert lib.tq_append_quantize(None, 1, 0, 1, 1, 128, 0, 0, 0, 3, 0, None, None,
+                                  None, None, 0, 4, 0, None) == _lib.TQ_OK
+
+
+def test_attention_rejects_unsupported_dim_and_bad_heads():
+    lib = _lib.load()
+    args = [None, 2, 1, 32, 8, 1, 96, 0, 0, 0, 0.1, 0, 0, None, None, None, None, 0, 3, 3,
+            None, None, 0, None, None, 16, 16, None, 0, None, None, 0, None]
+    assert lib.tq_attention(*args) == _lib.TQ_ERR_UNSUPPORTED
+    args[6] = 128
+    args[4] = 7
+    assert lib.tq_attention(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
+    args[4] = 8
+    args[18] = 5  # k_bits
+    assert lib.tq_attention(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
+
+
+def test_check_maps_status_to_exceptions():
+    lib = _lib.load()
+    lib.tq_packed_width(1, 1)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.TQ_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.TQ_ERR_UNSUPPORTED, "x")
+    with pytest.raises(_lib.TurboQuantLibraryError):
+        _lib.check(_lib.TQ_ERR_HIP, "x")

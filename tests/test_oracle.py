@@ -1,0 +1,310 @@
+"""Pin the CPU oracle (oracle/tq_oracle.py) to independent facts.
+
+Each check is chosen so that a plausible slip in the restatement (a dropped
+term, a wrong sign or index, a transposed operand, a wrong stage order) fails
+it: closed forms (Sylvester Hadamard from scipy), published tables (Max 1960),
+float64 quadrature of the Beta density, brute-force nearest-centroid search,
+hand-computed packed words, and torch SDPA on the dequantized cache.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+
+# ------------------------------------------------------------------ signs ---
+def test_sign_vector_known_prefix():
+    # numpy PCG64 stream for default_rng(0 + 128*7919).choice([-1, 1]), the
+    # reference's seeding (turboquant_cache.py:3545-3546).
+    want = [-1, -1, -1, -1, 1, -1, -1, -1, -1, 1, -1, -1, 1, 1, -1, -1]
+    assert O.rht_signs(128, 0)[:16].tolist() == want
+    s = O.rht_signs(256, 1)
+    assert s.dtype == np.float32 and set(np.unique(s)) == {-1.0, 1.0}
+    assert not np.array_equal(O.rht_signs(128, 0), O.rht_signs(128, 1))
+
+
+# --------------------------------------------------------------- rotation ---
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_rotation_orthogonal_and_sign_fixed(d):
+    R = O.rotation_matrix(d, 0).astype(np.float64)
+    assert np.abs(R.T @ R - np.eye(d)).max() < 2e-5
+    assert abs(abs(np.linalg.det(R)) - 1.0) < 1e-3
+    # sign fix: Q' = Q diag(sign(diag r)) makes diag(Q'^T M) = |diag r| > 0
+    M = np.random.default_rng(0 + d * 7919).standard_normal((d, d), dtype=np.float32)
+    assert (np.diag(R.T @ M.astype(np.float64)) > 0).all()
+
+
+# --------------------------------------------------------------- codebooks ---
+MAX_1960 = {
+    1: [0.7979],
+    2: [0.4528, 1.5104],
+    3: [0.2451, 0.7560, 1.3440, 2.1520],
+    4: [0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6181, 2.0690, 2.7326],
+}
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_gaussian_lloyd_max_matches_published_table(bits):
+    c = O.gaussian_lloyd_max(bits)
+    pos = c[len(c) // 2:]
+    np.testing.assert_allclose(pos, MAX_1960[bits], atol=6e-4)
+    np.testing.assert_allclose(c, -c[::-1], atol=1e-12)
+
+
+def _beta_cell_mean(d, a, b):
+    from scipy.integrate import quad
+    from scipy.special import gammaln
+
+    logc = gammaln(d / 2) - 0.5 * math.log(math.pi) - gammaln((d - 1) / 2)
+    pdf = lambda x: math.exp(logc + (d - 3) / 2 * math.log(max(1 - x * x, 1e-300)))
+    m0 = quad(pdf, a, b, limit=200)[0]
+    m1 = quad(lambda x: x * pdf(x), a, b, limit=200)[0]
+    return m1 / m0
+
+
+@pytest.mark.parametrize("d,bits", [(64, 2), (128, 3), (128, 4), (256, 2)])
+def test_beta_codebook_centroid_condition(d, bits):
+    """Each level is (close to) the conditional mean of its cell under the exact pdf.
+
+    The reference stops after at most 100 Lloyd iterations on a 32768-point
+    grid, so the 16-level books sit ~0.3% of a cell away from the fixed point;
+    a wrong density exponent ((d-1)/2 instead of (d-3)/2) moves levels ~9%.
+    """
+    c = O.beta_codebook(d, bits).astype(np.float64)
+    edges = np.concatenate([[-1.0], 0.5 * (c[:-1] + c[1:]), [1.0]])
+    means = np.array([_beta_cell_mean(d, edges[i], edges[i + 1]) for i in range(len(c))])
+    spacing = np.diff(c).min()
+    assert np.abs(means - c).max() < 1e-2 * spacing
+
+
+def test_beta_codebook_matches_survey_probe_and_gaussian_shape():
+    c = O.beta_codebook(128, 3) * math.sqrt(128)
+    np.testing.assert_allclose(
+        c, [-2.1302, -1.3352, -0.7521, -0.2443, 0.2433, 0.7515, 1.3345, 2.1296], atol=2e-4)
+    for d, b in [(128, 1), (128, 2), (256, 3), (256, 4)]:
+        cb = O.beta_codebook(d, b) * math.sqrt(d)
+        g = O.gaussian_lloyd_max(b)
+        assert np.all(np.diff(cb) > 0)
+        assert np.abs(cb - g).max() / np.abs(g).max() < 0.03
+    # centre midpoints of the slightly asymmetric f32 solution
+    assert abs(O.midpoints(O.beta_codebook(128, 3))[3] - (-4.54681e-05)) < 1e-10
+    assert O.midpoints(O.beta_codebook(128, 1))[0] == 0.0
+
+
+# ---------------------------------------------------------------- Hadamard ---
+@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
+def test_fwht_matches_sylvester_closed_form(d):
+    from scipy.linalg import hadamard
+
+    x = np.random.default_rng(d).standard_normal((5, d)).astype(np.float32)
+    want = x.astype(np.float64) @ hadamard(d).T
+    got = O.fwht_f32(x)
+    assert np.abs(got - want).max() < 1e-5 * math.sqrt(d) * np.abs(x).max()
+
+
+def test_fwht_planted_mistake_is_caught():
+    """A butterfly with (a+b, b-a) instead of (a+b, a-b) must fail the closed form."""
+    from scipy.linalg import hadamard
+
+    def bad(v):
+        v = v.copy()
+        d = v.shape[-1]
+        h = 1
+        while h < d:
+            w = v.reshape(-1, d // (2 * h), 2, h)
+            a, b = w[:, :, 0, :], w[:, :, 1, :]
+            v = np.stack([a + b, b - a], axis=2).reshape(-1, d)
+            h *= 2
+        return v
+
+    x = np.random.default_rng(3).standard_normal((2, 64)).astype(np.float32)
+    assert np.abs(bad(x) - x @ hadamard(64).T).max() > 1.0
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_rht_round_trip_and_basis_vector(d):
+    s = O.rht_signs(d, 0)
+    x = np.random.default_rng(1).standard_normal((4, d)).astype(np.float32)
+    np.testing.assert_allclose(O.rht_inverse_f32(O.rht_forward_f32(x, s), s), x, atol=1e-5)
+    np.testing.assert_allclose(O.rht_forward_f32(x, s), O.rht_forward_f64(x, s), atol=1e-5)
+    e0 = np.zeros(d, np.float32)
+    e0[0] = 1.0
+    y = O.rht_forward_f32(e0, s)
+    assert np.all(y == s[0] * np.float32(1.0 / math.sqrt(d)))
+
+
+# -------------------------------------------------------------------- norm ---
+def _norm_scalar_tree(x):
+    """The append kernel's reduction written out with scalar f32 arithmetic."""
+    f = np.float32
+    d = len(x)
+    lanes = []
+    for g in range(max(1, d // 32)):
+        s = [f(x[32 * g + i]) * f(x[32 * g + i]) for i in range(min(32, d))]
+        w = len(s) // 2
+        while w >= 1:
+            s = [f(s[i] + s[i + w]) for i in range(w)]
+            w //= 2
+        lanes.append(s[0])
+    while len(lanes) > 1:
+        lanes = [f(lanes[i] + lanes[i + 1]) for i in range(0, len(lanes), 2)]
+    return f(np.sqrt(lanes[0]))
+
+
+@pytest.mark.parametrize("d", [32, 128, 256])
+def test_norm_tree_order_and_accuracy(d):
+    x = (np.random.default_rng(d).standard_normal((6, d)) * 3).astype(np.float32)
+    got = O.norm_f32(x)
+    for i in range(6):
+        assert got[i] == _norm_scalar_tree(x[i])
+    np.testing.assert_allclose(got, np.linalg.norm(x.astype(np.float64), axis=-1), rtol=1e-6)
+    v = np.zeros(d, np.float32)
+    v[:2] = [3, 4]
+    assert O.norm_f32(v) == 5.0
+
+
+# ---------------------------------------------------------------- quantize ---
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_indices_match_brute_force_nearest_centroid(bits):
+    cb = O.beta_codebook(128, bits)
+    y = (np.random.default_rng(bits).standard_normal(20000) / math.sqrt(128)).astype(np.float32)
+    idx = O.quantize_indices(y, O.midpoints(cb))
+    dist = np.abs(y[:, None].astype(np.float64) - cb[None, :].astype(np.float64))
+    near = dist.argmin(axis=1)
+    mids = O.midpoints(cb).astype(np.float64)
+    clear = np.abs(y[:, None] - mids[None, :]).min(axis=1) > 1e-7
+    assert np.array_equal(idx[clear], near[clear])
+
+
+def test_strict_compare_tie_goes_low():
+    cb = O.beta_codebook(128, 2)
+    m = O.midpoints(cb)
+    idx = O.quantize_indices(m, m)  # y exactly at each midpoint
+    assert idx.tolist() == [0, 1, 2]
+
+
+@pytest.mark.parametrize("d,bits,want", [(128, 1, 0), (128, 2, 2), (128, 3, 4), (128, 4, 8),
+                                         (256, 1, 1), (256, 3, 3), (256, 4, 7)])
+def test_zero_vector_indices(d, bits, want):
+    # the f32 Beta codebooks are not exactly symmetric, so 0.0 lands on the
+    # side of the centre midpoint's sign (documented in the survey)
+    p, n = O.quantize_rht(np.zeros((1, d), np.float32), bits, O.rht_signs(d, 0),
+                          O.beta_codebook(d, bits))
+    assert n[0] == 0.0
+    assert np.all(O.unpack_lowbit(p, bits, d) == want)
+
+
+@pytest.mark.parametrize("d,bits", [(64, 3), (128, 2), (256, 4)])
+def test_quantize_against_float64_pipeline(d, bits):
+    x = np.random.default_rng(d + bits).standard_normal((64, d)).astype(np.float32)
+    s = O.rht_signs(d, 0)
+    cb = O.beta_codebook(d, bits)
+    p, n = O.quantize_rht(x, bits, s, cb)
+    u = x.astype(np.float64) / np.linalg.norm(x.astype(np.float64), axis=-1, keepdims=True)
+    y = O.rht_forward_f64(u, s)
+    near = np.abs(y[..., None] - cb.astype(np.float64)).argmin(-1)
+    mids = O.midpoints(cb).astype(np.float64)
+    clear = np.abs(y[..., None] - mids).min(-1) > 1e-6
+    got = O.unpack_lowbit(p, bits, d)
+    assert np.array_equal(got[clear], near[clear])
+    assert clear.mean() > 0.99
+
+
+# ------------------------------------------------------------------ packing ---
+def test_pack_hand_computed_words():
+    codes = np.zeros((1, 32), np.uint32)
+    codes[0, :8] = np.arange(8)
+    w = O.pack_lowbit(codes, 3)
+    assert w.shape == (1, 3) and w[0, 0] == 0x00FAC688 and w[0, 1] == 0 and w[0, 2] == 0
+    codes = np.zeros((1, 32), np.uint32)
+    codes[0, 10] = 7  # bits 30..32 straddle words 0 and 1
+    w = O.pack_lowbit(codes, 3)
+    assert w[0, 0] == 0xC0000000 and w[0, 1] == 1
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_pack_matches_bigint_and_round_trips(bits, d):
+    rng = np.random.default_rng(bits * d)
+    codes = rng.integers(0, 1 << bits, size=(7, d)).astype(np.uint32)
+    w = O.pack_lowbit(codes, bits)
+    assert w.shape == (7, (d * bits + 31) // 32)
+    for r in range(7):
+        big = sum(int(c) << (i * bits) for i, c in enumerate(codes[r]))
+        want = [(big >> (32 * k)) & 0xFFFFFFFF for k in range(w.shape[1])]
+        assert w[r].tolist() == want
+    assert np.array_equal(O.unpack_lowbit(w, bits, d), codes)
+
+
+# ---------------------------------------------------------------- attention ---
+def _attn_case(rng, B, Hq, Hkv, L, T, d, kb, vb, rot):
+    k = rng.standard_normal((B, Hkv, T, d)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, T, d)).astype(np.float32)
+    if rot == "hadamard":
+        kr, vr = O.rht_signs(d, 0), O.rht_signs(d, 1)
+        kp, kn = O.quantize_rht(k, kb, kr, O.beta_codebook(d, kb))
+        vp, vn = O.quantize_rht(v, vb, vr, O.beta_codebook(d, vb))
+    else:
+        kr, vr = O.rotation_matrix(d, 0), O.rotation_matrix(d, 1)
+        kp, kn, _ = O.quantize_dense(k, kb, kr, O.beta_codebook(d, kb))
+        vp, vn, _ = O.quantize_dense(v, vb, vr, O.beta_codebook(d, vb))
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, d)).astype(np.float32), "bf16")
+    return q, kp, kn, vp, vn, kr, vr
+
+
+@pytest.mark.parametrize("rot", ["hadamard", "dense"])
+def test_attention_equals_sdpa_on_dequantized_cache(rot):
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, L, T, d, kb, vb = 2, 4, 2, 3, 40, 64, 3, 2
+    q, kp, kn, vp, vn, kr, vr = _attn_case(rng, B, Hq, Hkv, L, T, d, kb, vb, rot)
+    scale = 1 / math.sqrt(d)
+    got = O.attention(q, kp, kn, vp, vn, k_bits=kb, v_bits=vb, k_codebook=O.beta_codebook(d, kb),
+                      v_codebook=O.beta_codebook(d, vb), rot_kind=rot, k_rot=kr, v_rot=vr,
+                      scale=scale, q_dtype="bf16", causal=True)
+    K = O.dequantize(kp, kn, kb, d, O.beta_codebook(d, kb), rot, kr)
+    V = O.dequantize(vp, vn, vb, d, O.beta_codebook(d, vb), rot, vr)
+    qs = O.scale_queries(q, scale, "bf16").astype(np.float64)
+    R = Hq // Hkv
+    Kt = torch.from_numpy(K).repeat_interleave(R, dim=1)
+    Vt = torch.from_numpy(V).repeat_interleave(R, dim=1)
+    mask = torch.arange(T)[None, :] <= (T - L + torch.arange(L))[:, None]
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(qs), Kt, Vt, attn_mask=mask, scale=1.0).numpy()
+    np.testing.assert_allclose(got, want, atol=1e-9)
+
+
+def test_decode_is_last_causal_row_and_f32_chunked_agrees():
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, L, T, d, kb, vb = 1, 8, 2, 4, 300, 128, 3, 3
+    q, kp, kn, vp, vn, kr, vr = _attn_case(rng, B, Hq, Hkv, L, T, d, kb, vb, "hadamard")
+    kw = dict(k_bits=kb, v_bits=vb, k_codebook=O.beta_codebook(d, kb),
+              v_codebook=O.beta_codebook(d, vb), rot_kind="hadamard", k_rot=kr, v_rot=vr,
+              scale=1 / math.sqrt(d), q_dtype="bf16")
+    full = O.attention(q, kp, kn, vp, vn, causal=True, **kw)
+    last = O.attention(q[:, :, -1:], kp, kn, vp, vn, causal=False, **kw)
+    np.testing.assert_allclose(full[:, :, -1:], last, atol=1e-12)
+    f32 = O.attention_chunked_f32(q, kp, kn, vp, vn, k_bits=kb, v_bits=vb,
+                                  k_codebook=O.beta_codebook(d, kb), v_codebook=O.beta_codebook(d, vb),
+                                  signs_k=kr, signs_v=vr, scale=1 / math.sqrt(d), q_dtype="bf16",
+                                  causal=True, key_chunk=128)
+    np.testing.assert_allclose(f32, full, atol=2e-5)
+
+
+def test_ragged_lengths_equal_truncated_cache():
+    rng = np.random.default_rng(13)
+    B, Hq, Hkv, L, T, d = 2, 4, 2, 1, 50, 64
+    q, kp, kn, vp, vn, kr, vr = _attn_case(rng, B, Hq, Hkv, L, T, d, 2, 2, "hadamard")
+    kw = dict(k_bits=2, v_bits=2, k_codebook=O.beta_codebook(d, 2), v_codebook=O.beta_codebook(d, 2),
+              rot_kind="hadamard", k_rot=kr, v_rot=vr, scale=0.125, q_dtype="bf16")
+    rag = O.attention(q, kp, kn, vp, vn, lengths=[20, 50], **kw)
+    cut = O.attention(q[:1], kp[:1, :, :20], kn[:1, :, :20], vp[:1, :, :20], vn[:1, :, :20], **kw)
+    np.testing.assert_allclose(rag[:1], cut, atol=1e-12)
+
+
+def test_bf16_rounding_matches_torch():
+    x = np.random.default_rng(5).standard_normal(10000).astype(np.float32) * 100
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.round_to_dtype(x, "bf16"), want)
