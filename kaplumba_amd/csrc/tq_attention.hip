@@ -1,8 +1,9 @@
 // Dense-rotation query preparation, split planning and the C-ABI entry of
 // attention.  The attention work itself is the fused kernel of tq_attn_impl.h.
 #include <algorithm>
+#include <cstdlib>
 
-#include "tq_attention.h"
+#include "tq_attn_merge.h"
 
 namespace tq {
 
@@ -32,19 +33,28 @@ __global__ __launch_bounds__(256) void qprep_kernel(AttnParams p) {
 }
 
 // ------------------------------------------------------------- planning ---
-SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T) {
+SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D) {
   SplitPlan sp{};
   const int R = Hq / Hkv;
   const int rows = R * L;
+  // query rows per workgroup; d = 256 keeps two so q and o fit in registers
+  const int nq_max = D >= 256 ? 2 : 4;
   sp.nq = rows >= 4 ? 4 : (rows >= 2 ? 2 : 1);
+  if (sp.nq > nq_max) sp.nq = nq_max;
   sp.n_rg = (rows + sp.nq - 1) / sp.nq;
   const int64_t base = static_cast<int64_t>(B) * Hkv * sp.n_rg;
-  const int64_t target = 4LL * device_cu_count();
+  // workgroups in flight per CU the split count aims for (KAPLUMBA_TQ_WG_PER_CU)
+  static const int per_cu = [] {
+    const char* e = getenv("KAPLUMBA_TQ_WG_PER_CU");
+    const int v = e ? atoi(e) : 1;
+    return v >= 1 && v <= 64 ? v : 1;
+  }();
+  const int64_t target = static_cast<int64_t>(per_cu) * device_cu_count();
   int64_t ns = base > 0 ? (target + base - 1) / base : 1;
-  const int64_t max_by_tokens = std::max<int64_t>(1, (T + 63) / 64);
+  const int64_t max_by_tokens = std::max<int64_t>(1, (T + 255) / 256);
   ns = std::max<int64_t>(1, std::min(ns, max_by_tokens));
   int64_t chunk = (T + ns - 1) / ns;
-  chunk = std::max<int64_t>(64, (chunk + 63) / 64 * 64);
+  chunk = std::max<int64_t>(256, (chunk + 255) / 256 * 256);  // 4 waves x 64-token sub-chunks
   chunk = std::min<int64_t>(chunk, kMaxChunk);
   sp.chunk = static_cast<int>(chunk);
   sp.n_splits = static_cast<int>(std::max<int64_t>(1, (T + chunk - 1) / chunk));
@@ -53,18 +63,19 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T) {
 
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Layout: [counters kCounterBytes][q_rot rows*D][partial o rows*splits*D][partial (m,l)].
+// Layout: [counters kCounterBytes][q_rot B*Hq*L*D][partial o groups*splits*nq*D]
+// [partial (m, l) groups*splits*nq*2], groups = B * Hkv * n_rg.
 int64_t workspace_bytes(const SplitPlan& sp, int B, int Hq, int Hkv, int L, int D) {
-  (void)Hkv;
   const int64_t rows = static_cast<int64_t>(B) * Hq * L;
-  return kCounterBytes + align256(rows * D * 4) + align256(rows * sp.n_splits * D * 4) +
-         align256(rows * sp.n_splits * 2 * 4);
+  const int64_t grows = static_cast<int64_t>(B) * Hkv * sp.n_rg * sp.nq;  // padded rows
+  return kCounterBytes + align256(rows * D * 4) + align256(grows * sp.n_splits * D * 4) +
+         align256(grows * sp.n_splits * 2 * 4);
 }
 
 size_t attn_lds_bytes(const SplitPlan& sp, int D) {
-  const size_t w = static_cast<size_t>(sp.chunk) * sp.nq;
-  const size_t o = static_cast<size_t>(kAttnWaves) * sp.nq * D;
-  const size_t m = static_cast<size_t>(sp.n_splits) * sp.nq;
+  const size_t w = static_cast<size_t>(sp.chunk) * sp.nq;               // scores / weights
+  const size_t o = static_cast<size_t>(kAttnWaves) * sp.nq * D;         // wave fold
+  const size_t m = static_cast<size_t>(merge_scratch_floats(sp.nq, D));  // merge scratch
   return std::max(w, std::max(o, m)) * sizeof(float);
 }
 
@@ -76,7 +87,7 @@ extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, in
                                                int64_t max_tokens) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || dim <= 0 || max_tokens < 0 || Hq % Hkv)
     return 0;
-  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, std::max<int64_t>(max_tokens, 1));
+  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, std::max<int64_t>(max_tokens, 1), dim);
   return workspace_bytes(sp, B, Hq, Hkv, L, dim);
 }
 
@@ -119,7 +130,7 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   if (!q || !out || !workspace) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null pointer");
   if (max_tokens > 0 && (!k || !v)) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null cache pointer");
   const int64_t T = std::max<int64_t>(max_tokens, 1);
-  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, T);
+  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, T, dim);
   if (static_cast<int64_t>(B) * Hkv * sp.n_rg > kMaxGroups)
     return fail(TQ_ERR_UNSUPPORTED, "attention: %lld (batch, kv head, row group) groups > %d",
                 (long long)B * Hkv * sp.n_rg, kMaxGroups);
@@ -171,7 +182,7 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   p.qrot = reinterpret_cast<float*>(ws);
   ws += (rows * dim * 4 + 255) / 256 * 256;
   p.po = reinterpret_cast<float*>(ws);
-  ws += (rows * sp.n_splits * dim * 4 + 255) / 256 * 256;
+  ws += (static_cast<int64_t>(B) * Hkv * sp.n_rg * sp.nq * sp.n_splits * dim * 4 + 255) / 256 * 256;
   p.pml = reinterpret_cast<float*>(ws);
   p.out = out;
 

@@ -23,7 +23,8 @@
 // Plain (fp16/bf16) caches use the same passes with direct element loads.
 #pragma once
 
-#include "tq_attention.h"
+#include "tq_attn_merge.h"
+#include "tq_attn_tq.h"
 
 namespace tq {
 
@@ -41,45 +42,6 @@ __device__ __forceinline__ void unpack8(const uint4 t, float* v) {
       v[2 * j] = bf16_bits_to_f32(lo);
       v[2 * j + 1] = bf16_bits_to_f32(hi);
     }
-  }
-}
-
-__device__ __forceinline__ float load_q(const void* q, int dt, int64_t i) {
-  if (dt == TQ_DTYPE_F32) return static_cast<const float*>(q)[i];
-  const uint16_t h = static_cast<const uint16_t*>(q)[i];
-  return dt == TQ_DTYPE_F16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
-}
-
-__device__ __forceinline__ float round_q(int dt, float v) {
-  if (dt == TQ_DTYPE_F32) return v;
-  return dt == TQ_DTYPE_F16 ? round_to<TQ_DTYPE_F16>(v) : round_to<TQ_DTYPE_BF16>(v);
-}
-
-__device__ __forceinline__ void store_out(void* o, int dt, int64_t i, float v) {
-  if (dt == TQ_DTYPE_F32)
-    static_cast<float*>(o)[i] = v;
-  else if (dt == TQ_DTYPE_F16)
-    static_cast<uint16_t*>(o)[i] = f32_to_f16_bits(v);
-  else
-    static_cast<uint16_t*>(o)[i] = f32_to_bf16_bits(v);
-}
-
-// In-place unnormalised Walsh-Hadamard transform of NQ rows of length D in
-// LDS (stride D), all threads of the block participating.
-template <int D, int NQ>
-__device__ __forceinline__ void lds_fwht(float* y) {
-#pragma unroll 1
-  for (int hs = 1; hs < D; hs <<= 1) {
-    for (int idx = threadIdx.x; idx < NQ * D / 2; idx += kAttnThreads) {
-      const int j = idx / (D / 2);
-      const int k = idx % (D / 2);
-      const int i0 = (k / hs) * 2 * hs + (k % hs);
-      const float a = y[j * D + i0];
-      const float b = y[j * D + i0 + hs];
-      y[j * D + i0] = a + b;
-      y[j * D + i0 + hs] = a - b;
-    }
-    __syncthreads();
   }
 }
 
@@ -103,6 +65,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnParams p
   __shared__ float s_kcb[16];
   __shared__ float s_vcb[16];
   __shared__ float s_red[kAttnWaves][NQ];
+  __shared__ float s_ml[2 * NQ];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -374,19 +337,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnParams p
       for (int e = 0; e < CGV; ++e) s_o[(wave * NQ + j) * D + gV * CGV + e] = o[j][e];
   }
   __syncthreads();
-  const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;
+  // combine the waves into s_q and hand over to the split publication / merge
   for (int idx = tid; idx < NQ * D; idx += kAttnThreads) {
-    const int j = idx / D;
-    const int d = idx % D;
-    if (rg * NQ + j >= rows) continue;
-    float s = s_o[j * D + d];
+    float a = 0.f;
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) s += s_o[(w * NQ + j) * D + d];
-    const int rr = rg * NQ + j;
-    const int64_t qo = (static_cast<int64_t>(b) * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L;
-    p.po[(qo * p.n_splits + split) * D + d] = s;
+    for (int w = 0; w < kAttnWaves; ++w) a += s_o[w * NQ * D + idx];
+    s_q[idx] = a;
   }
-  if (tid < NQ && rg * NQ + tid < rows) {
+  if (tid < NQ) {
     float mv = mrow[0], lv = ltot[0];
 #pragma unroll
     for (int jj = 1; jj < NQ; ++jj)
@@ -394,116 +352,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnParams p
         mv = mrow[jj];
         lv = ltot[jj];
       }
-    const int rr = rg * NQ + tid;
-    const int64_t qo = (static_cast<int64_t>(b) * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L;
-    p.pml[(qo * p.n_splits + split) * 2 + 0] = mv;
-    p.pml[(qo * p.n_splits + split) * 2 + 1] = lv;
-  }
-
-  // ------------------------------------------------------------- merge ----
-  // Publish this split, then let the last workgroup of the group merge.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(p.counters + grp, 1u, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev + 1 == static_cast<uint32_t>(nvalid)) ? 1 : 0;
+    s_ml[2 * tid] = mv;
+    s_ml[2 * tid + 1] = lv;
   }
   __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (tid == 0)
-    __hip_atomic_store(p.counters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-  float* s_sc = smem;  // [NQ][nvalid] split scales
-  // per-row global max
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    float m = -INFINITY;
-    if (rvalid[j])
-      for (int sp = tid; sp < nvalid; sp += kAttnThreads)
-        m = fmaxf(m, __builtin_nontemporal_load(p.pml + (qoff[j] * p.n_splits + sp) * 2));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-    if (lane == 0) s_red[wave][j] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    float m = s_red[0][j];
-#pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) m = fmaxf(m, s_red[w][j]);
-    mrow[j] = m;
-  }
-  __syncthreads();
-  // split scales and the total normaliser
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    float l = 0.f;
-    if (rvalid[j])
-      for (int sp = tid; sp < nvalid; sp += kAttnThreads) {
-        const float* e = p.pml + (qoff[j] * p.n_splits + sp) * 2;
-        const float sc = __expf(__builtin_nontemporal_load(e) - mrow[j]);
-        s_sc[j * nvalid + sp] = sc;
-        l += sc * __builtin_nontemporal_load(e + 1);
-      }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, kWave);
-    if (lane == 0) s_red[wave][j] = l;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    float l = s_red[0][j];
-#pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) l += s_red[w][j];
-    ltot[j] = l;
-  }
-  // weighted sum of the split outputs, normalised, into s_q
-  for (int idx = tid; idx < NQ * D; idx += kAttnThreads) {
-    const int j = idx / D;
-    const int d = idx % D;
-    float acc = 0.f;
-    float lt = ltot[0];
-    int64_t qo = qoff[0];
-    bool ok = rvalid[0];
-#pragma unroll
-    for (int jj = 1; jj < NQ; ++jj)
-      if (jj == j) {
-        lt = ltot[jj];
-        qo = qoff[jj];
-        ok = rvalid[jj];
-      }
-    if (ok) {
-      const float* src = p.po + qo * p.n_splits * D + d;
-      for (int sp = 0; sp < nvalid; ++sp)
-        acc = fmaf(s_sc[j * nvalid + sp], __builtin_nontemporal_load(src + static_cast<int64_t>(sp) * D), acc);
-    }
-    s_q[idx] = acc / fmaxf(lt, kNormEps);
-  }
-  __syncthreads();
-  // inverse rotation and store
-  if constexpr (!PLAIN) {
-    if (!dense) lds_fwht<D, NQ>(s_q);
-  }
-  for (int idx = tid; idx < NQ * D; idx += kAttnThreads) {
-    const int j = idx / D;
-    const int d = idx % D;
-    if (rg * NQ + j >= rows) continue;
-    const int rr = rg * NQ + j;
-    const int64_t qo = (static_cast<int64_t>(b) * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L;
-    float r = s_q[idx];
-    if constexpr (!PLAIN) {
-      if (!dense) {
-        r = r * p.rscale * p.vrot[d];
-      } else {
-        float a2 = 0.f;  // x_d = sum_k y_k R[k][d]
-        for (int k2 = 0; k2 < D; ++k2) a2 = fmaf(s_q[j * D + k2], p.vrot[static_cast<int64_t>(k2) * D + d], a2);
-        r = a2;
-      }
-    }
-    store_out(p.out, p.q_dtype, qo * D + d, r);
-  }
+  RowSet<NQ> rs;
+  rs.init(p, b, gk, rg);
+  const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;
+  publish_and_merge<D, NQ>(p, rs, s_q, s_ml, smem, &s_last, grp, split, nvalid, PLAIN, dense);
 }
 
 template <int D, int KB, int VB, int KVDT>
@@ -519,21 +375,48 @@ int launch_partial_nq(const AttnParams& p, hipStream_t st) {
       hipLaunchKernelGGL((attn_partial_kernel<D, KB, VB, 2, KVDT>), grid, dim3(kAttnThreads), lds, st, p);
       break;
     case 4:
-      hipLaunchKernelGGL((attn_partial_kernel<D, KB, VB, 4, KVDT>), grid, dim3(kAttnThreads), lds, st, p);
-      break;
+      if constexpr (D < 256) {  // the planner caps D >= 256 at two rows (register budget)
+        hipLaunchKernelGGL((attn_partial_kernel<D, KB, VB, 4, KVDT>), grid, dim3(kAttnThreads), lds, st, p);
+        break;
+      }
+      [[fallthrough]];
     default:
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: rows per group %d", p.nq);
   }
   return check_launch("attn_partial_kernel");
 }
 
+template <int D, int KB, int VB>
+int launch_tq_nq(const AttnParams& p, hipStream_t st) {
+  const dim3 grid(p.n_splits, p.Hkv * p.n_rg, p.B);
+  const SplitPlan sp{p.n_splits, p.chunk, p.n_rg, p.nq};
+  const size_t lds = attn_lds_bytes(sp, D);
+  switch (p.nq) {
+    case 1:
+      hipLaunchKernelGGL((attn_tq_kernel<D, KB, VB, 1>), grid, dim3(kAttnThreads), lds, st, p);
+      break;
+    case 2:
+      hipLaunchKernelGGL((attn_tq_kernel<D, KB, VB, 2>), grid, dim3(kAttnThreads), lds, st, p);
+      break;
+    case 4:
+      if constexpr (D < 256) {  // the planner caps D >= 256 at two rows (register budget)
+        hipLaunchKernelGGL((attn_tq_kernel<D, KB, VB, 4>), grid, dim3(kAttnThreads), lds, st, p);
+        break;
+      }
+      [[fallthrough]];
+    default:
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: rows per group %d", p.nq);
+  }
+  return check_launch("attn_tq_kernel");
+}
+
 template <int D, int KB>
 int launch_partial_vb(const AttnParams& p, int vb, hipStream_t st) {
   switch (vb) {
-    case 1: return launch_partial_nq<D, KB, 1, TQ_DTYPE_F32>(p, st);
-    case 2: return launch_partial_nq<D, KB, 2, TQ_DTYPE_F32>(p, st);
-    case 3: return launch_partial_nq<D, KB, 3, TQ_DTYPE_F32>(p, st);
-    case 4: return launch_partial_nq<D, KB, 4, TQ_DTYPE_F32>(p, st);
+    case 1: return launch_tq_nq<D, KB, 1>(p, st);
+    case 2: return launch_tq_nq<D, KB, 2>(p, st);
+    case 3: return launch_tq_nq<D, KB, 3>(p, st);
+    case 4: return launch_tq_nq<D, KB, 4>(p, st);
   }
   return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
 }
