@@ -68,7 +68,7 @@ struct SplitPlan {
   int n_splits, chunk, n_rg, nq;
 };
 
-SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D);
+SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool packed);
 int64_t workspace_bytes(const SplitPlan& p, int B, int Hq, int Hkv, int L, int D);
 size_t attn_lds_bytes(const SplitPlan& p, int D);
 

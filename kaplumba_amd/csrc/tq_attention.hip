@@ -3,7 +3,7 @@
 #include <algorithm>
 #include <cstdlib>
 
-#include "tq_attn_merge.h"
+#include "tq_attn_splitmerge.h"
 
 namespace tq {
 
@@ -33,14 +33,20 @@ __global__ __launch_bounds__(256) void qprep_kernel(AttnParams p) {
 }
 
 // ------------------------------------------------------------- planning ---
-SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D) {
+SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool packed) {
   SplitPlan sp{};
   const int R = Hq / Hkv;
   const int rows = R * L;
-  // query rows per workgroup; d = 256 keeps two so q and o fit in registers
-  const int nq_max = D >= 256 ? 2 : 4;
-  sp.nq = rows >= 4 ? 4 : (rows >= 2 ? 2 : 1);
-  if (sp.nq > nq_max) sp.nq = nq_max;
+  if (packed) {
+    // matrix-core kernel: 16-row tiles; 4-row groups when the GQA group is
+    // small (less LDS and fewer partial rows), and for d = 256 (registers)
+    sp.nq = (rows <= 4 || D >= 256) ? 4 : 16;
+  } else {
+    // plain kernel: d = 256 keeps two rows so q and o fit in registers
+    const int nq_max = D >= 256 ? 2 : 4;
+    sp.nq = rows >= 4 ? 4 : (rows >= 2 ? 2 : 1);
+    if (sp.nq > nq_max) sp.nq = nq_max;
+  }
   sp.n_rg = (rows + sp.nq - 1) / sp.nq;
   const int64_t base = static_cast<int64_t>(B) * Hkv * sp.n_rg;
   // workgroups in flight per CU the split count aims for (KAPLUMBA_TQ_WG_PER_CU)
@@ -54,7 +60,7 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D) {
   const int64_t max_by_tokens = std::max<int64_t>(1, (T + 255) / 256);
   ns = std::max<int64_t>(1, std::min(ns, max_by_tokens));
   int64_t chunk = (T + ns - 1) / ns;
-  chunk = std::max<int64_t>(256, (chunk + 255) / 256 * 256);  // 4 waves x 64-token sub-chunks
+  chunk = std::max<int64_t>(256, (chunk + 255) / 256 * 256);  // whole sub-chunks for every wave
   chunk = std::min<int64_t>(chunk, kMaxChunk);
   sp.chunk = static_cast<int>(chunk);
   sp.n_splits = static_cast<int>(std::max<int64_t>(1, (T + chunk - 1) / chunk));
@@ -87,8 +93,10 @@ extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, in
                                                int64_t max_tokens) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || dim <= 0 || max_tokens < 0 || Hq % Hkv)
     return 0;
-  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, std::max<int64_t>(max_tokens, 1), dim);
-  return workspace_bytes(sp, B, Hq, Hkv, L, dim);
+  // large enough for either cache kind
+  const int64_t T = std::max<int64_t>(max_tokens, 1);
+  return std::max(workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, true), B, Hq, Hkv, L, dim),
+                  workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, false), B, Hq, Hkv, L, dim));
 }
 
 extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
@@ -106,6 +114,8 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
     return fail(TQ_ERR_UNSUPPORTED, "attention: dim %d not in {64, 128, 256}", dim);
   if (q_dtype != TQ_DTYPE_F32 && q_dtype != TQ_DTYPE_F16 && q_dtype != TQ_DTYPE_BF16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: q_dtype %d", q_dtype);
+  if (capacity > INT32_MAX)
+    return fail(TQ_ERR_UNSUPPORTED, "attention: capacity %lld above 2^31 - 1 tokens", (long long)capacity);
   if (max_tokens < 0 || max_tokens > capacity)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: max_tokens %lld > capacity %lld",
                 (long long)max_tokens, (long long)capacity);
@@ -120,6 +130,10 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null codec pointer");
     if (max_tokens > 0 && (!k_norms || !v_norms))
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null norms pointer");
+    // the kernel addresses one (sequence, kv head) row with 32-bit byte offsets
+    if (capacity * (static_cast<int64_t>(dim) * std::max(k_bits, v_bits) / 8) > UINT32_MAX)
+      return fail(TQ_ERR_UNSUPPORTED, "attention: a packed row of %lld tokens exceeds 4 GiB",
+                  (long long)capacity);
   } else if (kv_kind == TQ_KV_PLAIN) {
     if (kv_dtype != TQ_DTYPE_F16 && kv_dtype != TQ_DTYPE_BF16)
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: plain kv_dtype %d", kv_dtype);
@@ -130,7 +144,7 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   if (!q || !out || !workspace) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null pointer");
   if (max_tokens > 0 && (!k || !v)) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null cache pointer");
   const int64_t T = std::max<int64_t>(max_tokens, 1);
-  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, T, dim);
+  const SplitPlan sp = plan_splits(B, Hq, Hkv, L, T, dim, kv_kind == TQ_KV_PACKED);
   if (static_cast<int64_t>(B) * Hkv * sp.n_rg > kMaxGroups)
     return fail(TQ_ERR_UNSUPPORTED, "attention: %lld (batch, kv head, row group) groups > %d",
                 (long long)B * Hkv * sp.n_rg, kMaxGroups);
@@ -201,8 +215,17 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   }
   p.T = max_tokens;
   switch (dim) {
-    case 64: return launch_partial_d64(p, kv_kind, kv_dtype, k_bits, v_bits, st);
-    case 128: return launch_partial_d128(p, kv_kind, kv_dtype, k_bits, v_bits, st);
-    default: return launch_partial_d256(p, kv_kind, kv_dtype, k_bits, v_bits, st);
+    case 64: rc = launch_partial_d64(p, kv_kind, kv_dtype, k_bits, v_bits, st); break;
+    case 128: rc = launch_partial_d128(p, kv_kind, kv_dtype, k_bits, v_bits, st); break;
+    default: rc = launch_partial_d256(p, kv_kind, kv_dtype, k_bits, v_bits, st); break;
   }
+  if (rc || kv_kind != TQ_KV_PACKED || sp.n_splits == 1) return rc;
+  // packed caches: the splits' partials are merged by a second kernel
+  const dim3 mgrid(static_cast<unsigned>(sp.nq), static_cast<unsigned>(Hkv * sp.n_rg), static_cast<unsigned>(B));
+  switch (dim) {
+    case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mgrid, dim3(kMergeThreads), 0, st, p); break;
+    case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mgrid, dim3(kMergeThreads), 0, st, p); break;
+    default: hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(kMergeThreads), 0, st, p); break;
+  }
+  return check_launch("attn_merge_kernel");
 }

@@ -24,7 +24,7 @@
 #pragma once
 
 #include "tq_attn_merge.h"
-#include "tq_attn_tq.h"
+#include "tq_attn_mfma.h"
 
 namespace tq {
 
@@ -356,10 +356,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnParams p
     s_ml[2 * tid + 1] = lv;
   }
   __syncthreads();
-  RowSet<NQ> rs;
-  rs.init(p, b, gk, rg);
+  RowSet rs;
+  rs.init(p, b, gk, rg, NQ);
   const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;
-  publish_and_merge<D, NQ>(p, rs, s_q, s_ml, smem, &s_last, grp, split, nvalid, PLAIN, dense);
+  __shared__ float s_aux[NQ + D];
+  publish_and_merge<D, NQ>(p, rs, s_q, s_ml, smem, s_aux, &s_last, grp, split, nvalid, PLAIN, dense);
 }
 
 template <int D, int KB, int VB, int KVDT>
@@ -386,37 +387,13 @@ int launch_partial_nq(const AttnParams& p, hipStream_t st) {
   return check_launch("attn_partial_kernel");
 }
 
-template <int D, int KB, int VB>
-int launch_tq_nq(const AttnParams& p, hipStream_t st) {
-  const dim3 grid(p.n_splits, p.Hkv * p.n_rg, p.B);
-  const SplitPlan sp{p.n_splits, p.chunk, p.n_rg, p.nq};
-  const size_t lds = attn_lds_bytes(sp, D);
-  switch (p.nq) {
-    case 1:
-      hipLaunchKernelGGL((attn_tq_kernel<D, KB, VB, 1>), grid, dim3(kAttnThreads), lds, st, p);
-      break;
-    case 2:
-      hipLaunchKernelGGL((attn_tq_kernel<D, KB, VB, 2>), grid, dim3(kAttnThreads), lds, st, p);
-      break;
-    case 4:
-      if constexpr (D < 256) {  // the planner caps D >= 256 at two rows (register budget)
-        hipLaunchKernelGGL((attn_tq_kernel<D, KB, VB, 4>), grid, dim3(kAttnThreads), lds, st, p);
-        break;
-      }
-      [[fallthrough]];
-    default:
-      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: rows per group %d", p.nq);
-  }
-  return check_launch("attn_tq_kernel");
-}
-
 template <int D, int KB>
 int launch_partial_vb(const AttnParams& p, int vb, hipStream_t st) {
   switch (vb) {
-    case 1: return launch_tq_nq<D, KB, 1>(p, st);
-    case 2: return launch_tq_nq<D, KB, 2>(p, st);
-    case 3: return launch_tq_nq<D, KB, 3>(p, st);
-    case 4: return launch_tq_nq<D, KB, 4>(p, st);
+    case 1: return launch_mfma_nq<D, KB, 1>(p, st);
+    case 2: return launch_mfma_nq<D, KB, 2>(p, st);
+    case 3: return launch_mfma_nq<D, KB, 3>(p, st);
+    case 4: return launch_mfma_nq<D, KB, 4>(p, st);
   }
   return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
 }
