@@ -117,7 +117,7 @@ struct MfmaShape {
   static constexpr int NW = D >= 256 ? 4 : 8;
   static constexpr int NT = NW * kWave;
   static constexpr int SUB = 32;  // tokens per sub-chunk
-  static constexpr int P = 3;     // sub-chunks in flight per wave
+  static constexpr int P = 2;     // sub-chunks in flight per wave
   // scores
   static constexpr int KSPAN = D / 4;  // coordinates of one token per lane
   static constexpr int KPP = KSPAN / 4;  // 4-coordinate groups per lane span (MFMA pairs)
@@ -413,9 +413,10 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
 #pragma unroll
   for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
 
+  // only the first sub-chunk before the prologue: its transfer overlaps the
+  // prologue's work (the rest is issued after it, ahead of the loop)
   Buf buf[P];
-#pragma unroll
-  for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
+  load_sub(buf[0], sub_start(0));
 
   // ------------------------------------------------------------ prologue ----
   float kmax = 0.f, vmax = 0.f;
@@ -437,19 +438,38 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
         err = fmaxf(err, fabsf(static_cast<float>(static_cast<_Float16>(v)) - v) *
                              __builtin_amdgcn_rcpf(fabsf(v)));
     }
+    // argmin (smallest index on ties) over the 16 lanes of each row by DPP
+    // rotations, then over the four rows by lane reads
     int idx = tid;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float oe = __shfl_xor(err, off, kWave);
-      const int oi = __shfl_xor(idx, off, kWave);
+    for (int k = 0; k < 4; ++k) {
+      float oe;
+      int oi;
+      switch (k) {
+        case 0: oe = row_ror<8>(err); oi = __builtin_bit_cast(int, row_ror<8>(__builtin_bit_cast(float, idx))); break;
+        case 1: oe = row_ror<4>(err); oi = __builtin_bit_cast(int, row_ror<4>(__builtin_bit_cast(float, idx))); break;
+        case 2: oe = row_ror<2>(err); oi = __builtin_bit_cast(int, row_ror<2>(__builtin_bit_cast(float, idx))); break;
+        default: oe = row_ror<1>(err); oi = __builtin_bit_cast(int, row_ror<1>(__builtin_bit_cast(float, idx))); break;
+      }
       if (oe < err || (oe == err && oi < idx)) {
         err = oe;
         idx = oi;
       }
     }
+    float be = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, err), 0));
+    int bi = __builtin_amdgcn_readlane(idx, 0);
+#pragma unroll
+    for (int r = 1; r < 4; ++r) {
+      const float e2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, err), 16 * r));
+      const int i2 = __builtin_amdgcn_readlane(idx, 16 * r);
+      if (e2 < be || (e2 == be && i2 < bi)) {
+        be = e2;
+        bi = i2;
+      }
+    }
     if (lane == 0) {
-      s_serr[wave] = err;
-      s_sidx[wave] = idx;
+      s_serr[wave] = be;
+      s_sidx[wave] = bi;
     }
   }
 
@@ -583,6 +603,8 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   for (int i = 0; i < 4; ++i) lim_min = min(lim_min, lim[i]);
   for (int off = 16; off < 64; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, kWave));
   lds_barrier();
+#pragma unroll
+  for (int s = 1; s < P; ++s) load_sub(buf[s], sub_start(s));
 
   // ------------------------------------------------------------ streaming ----
   float m_run[4], l_run[4];
@@ -598,9 +620,14 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   float vsc = 0.f;  // 2^-E
   uint16_t* w_mine = s_w + wave * 16 * SUB;
 
-  auto process = [&](const Buf& bf, int s0) {
-    // ---- scores of the two 16-token tiles: four independent accumulator
-    // chains (tile x {q hi, q lo}) keep the matrix pipe busy
+  // Software pipeline: the scores of sub-chunk i + 1 are computed right after
+  // the value pass of sub-chunk i, in one region without fences, so their
+  // table lookups and matrix operations interleave (each alone is a long
+  // dependency chain).
+  //   scores(bf, Sc): raw q.k of the sub-chunk's two 16-token tiles
+  //   finish(bf, Sc, s0): scale and mask, online softmax, weights, values
+  auto scores = [&](const Buf& bf, f32x4_t (&Sc)[2]) {
+    // four independent accumulator chains (tile x {q hi, q lo})
     uint32_t al[2][KAL];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
@@ -627,9 +654,10 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
         Sb[tt] = mfma_f16(qb[j], bk[tt], Sb[tt]);
       }
     }
-    f32x4_t Sc[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) Sc[tt] = Sa[tt] + Sb[tt];
+  };
+  auto finish = [&](const Buf& bf, const f32x4_t (&Sc)[2], int s0) {
     float sv[2][4];  // scores in log2 units
     float nvt[2];
 #pragma unroll
@@ -651,45 +679,51 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
         }
       }
     }
-    // ---- online softmax, rows 4g + i over the 16 lanes of the row
-    float alpha[4], pw[2][4], cmx[4];
+    // ---- online softmax, rows 4g + i over the 16 lanes of the row.  Lazy
+    // reference max: m_run moves only when a row's sub-chunk max exceeds it
+    // by more than kLazy (log2 units), so exponents stay <= 2^kLazy and the
+    // accumulators are rescaled rarely (a wave-uniform branch).
+    constexpr float kLazy = 8.f;
+    float cmx[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) cmx[i] = fmaxf(sv[0][i], sv[1][i]);
     row16_max4(cmx);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float cm = cmx[i];
-      const float mn = fmaxf(m_run[i], cm);
-      alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - mn);  // exp2(-inf) = 0 on the first sub-chunk
-      pw[0][i] = __builtin_amdgcn_exp2f(sv[0][i] - mn);
-      pw[1][i] = __builtin_amdgcn_exp2f(sv[1][i] - mn);
-      l_run[i] = fmaf(l_run[i], alpha[i], pw[0][i] + pw[1][i]);
-      m_run[i] = mn;
-    }
-    // value-norm exponent (wave-uniform): keep w = p * ||v|| * 2^-E below 1
     const float nv0 = nvt[0];
     const float nv1 = nvt[1];
-    {
-      int e;
-      frexpf(row16_max(fmaxf(nv0, nv1)), &e);
-      if (e > E) {
-        const float f = ldexpf(1.f, E - e);
+    int enew;
+    frexpf(row16_max(fmaxf(nv0, nv1)), &enew);  // wave-uniform value-norm exponent
+    bool move = enew > E;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) alpha[i] *= f;
-        E = e;
-        vsc = ldexpf(1.f, -E);
+    for (int i = 0; i < 4; ++i) move |= cmx[i] > m_run[i] + kLazy;
+    if (__any(move ? 1 : 0)) {
+      float alpha[4];
+      const int e2 = enew > E ? enew : E;
+      const float f = ldexpf(1.f, E - e2);  // exact power of two (0 on the first sub-chunk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float mn = cmx[i] > m_run[i] + kLazy ? fmaxf(m_run[i], cmx[i]) : m_run[i];
+        alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - mn);  // exp2(-inf) = 0 on the first sub-chunk
+        l_run[i] *= alpha[i];
+        alpha[i] *= f;
+        m_run[i] = mn;
       }
-    }
-    bool rescale = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rescale |= alpha[i] != 1.f;
-    if (__any(rescale ? 1 : 0)) {
+      E = e2;
+      vsc = ldexpf(1.f, -E);
 #pragma unroll
       for (int c = 0; c < CPL; ++c)
 #pragma unroll
         for (int i = 0; i < 4; ++i) O[c][i] *= alpha[i];
     }
-    // ---- weights to LDS: [row][token] f16
+    float pw[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pw[0][i] = __builtin_amdgcn_exp2f(sv[0][i] - m_run[i]);
+      pw[1][i] = __builtin_amdgcn_exp2f(sv[1][i] - m_run[i]);
+      l_run[i] += pw[0][i] + pw[1][i];
+    }
+    // ---- weights to LDS: [row][token] f16 (after the previous sub-chunk's
+    // reads of the weight buffer)
+    wave_sync();
     if (4 * g < NQ) {
       const float f0 = nv0 * vsc;
       const float f1 = nv1 * vsc;
@@ -738,17 +772,21 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
       }
       O[c] = mfma_f16(A, bv, O[c]);
     }
-    wave_sync();
   };
 
   // Prefetches are issued unconditionally (past the end they are free), so
   // the compiler's count of outstanding loads is exact and each sub-chunk
   // waits for its own loads only.
+  f32x4_t Sc[2];
+  if (n_my > 0) scores(buf[0], Sc);
   for (int base = 0; base < n_my; base += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       const int i = base + s;
-      if (i < n_my) process(buf[s], sub_start(i));
+      if (i < n_my) {
+        finish(buf[s], Sc, sub_start(i));
+        if (i + 1 < n_my) scores(buf[(s + 1) % P], Sc);
+      }
       load_sub(buf[s], sub_start(i + P));
     }
   }
