@@ -32,7 +32,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 CFG1 = dict(B=1, Hq=32, Hkv=8, D=128, T=32768, bits=3)
+# config 2: ragged batched decode, d=256, K4/V2, dense 256x256 rotation
+CFG2 = dict(B=32, Hq=16, Hkv=8, D=256, kb=4, vb=2, lo=2048, hi=8192, seed=1004)
+# config 3: prefill append of one 8192-token chunk into a 36-layer cache
+CFG3 = dict(layers=36, plain_layers=4, Hkv=8, T=8192, D=128, bits=3)
+# config 4: speculative verify, 4 drafts per sequence, 131072 + 4 cached tokens, K2/V1
+CFG4 = dict(B=4, Hq=32, Hkv=8, L=4, T=131072 + 4, D=128, kb=2, vb=1)
 
 
 def algorithmic_decode_bytes(Hkv, T, D, kb, vb, norm_bytes, B=1):
@@ -149,6 +156,200 @@ def bench_quantize(torch, args, dev):
     return dict(bytes=per_call, ms_per_step=ms, kernel_bytes=per_call / 2)
 
 
+def _free(torch):
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def _synth_kv(torch, g, shape, dtype, dev):
+    """N(0,1) x per-(kv head, channel) log-normal(0, 0.5) scales, like config 0."""
+    B, H, T, D = shape
+    scale = torch.exp(torch.randn(1, H, 1, D, device=dev, generator=g) * 0.5)
+    return [(torch.randn(shape, device=dev, generator=g) * scale).to(dtype) for _ in range(2)]
+
+
+def bench_ragged(torch, args, dev):
+    """Config 2: 32 sequences of U[2048, 8192] tokens, d=256, K4/V2, dense rotation."""
+    import numpy as np
+
+    from kaplumba_amd import ops
+
+    c = CFG2
+    lens = np.random.default_rng(c["seed"]).integers(c["lo"], c["hi"] + 1, size=c["B"])
+    cap = c["hi"]
+    kc = ops.Codec(c["D"], c["kb"], 0, rotation="dense")
+    vc = ops.Codec(c["D"], c["vb"], 1, rotation="dense")
+    per_step = c["Hkv"] * int(lens.sum()) * (4 * kc.packed_width + 4 * vc.packed_width + 8)
+    n_sets = max(2, math.ceil(args.rotate_mb * 1e6 / per_step))
+    g = torch.Generator(device=dev).manual_seed(2000)
+    sets = []
+    for _ in range(n_sets):
+        st = []
+        for codec, x in zip((kc, vc), _synth_kv(torch, g, (c["B"], c["Hkv"], cap, c["D"]),
+                                                  torch.bfloat16, dev)):
+            pk = torch.empty((c["B"], c["Hkv"], cap, codec.packed_width), dtype=torch.uint32, device=dev)
+            nm = torch.empty((c["B"], c["Hkv"], cap), dtype=torch.float32, device=dev)
+            ops.append_quantize(x, codec, pk, nm, 0)
+            st.append((nm, pk))
+            del x
+        sets.append(st)
+        _free(torch)
+    qs = [torch.randn(c["B"], c["Hq"], 1, c["D"], device=dev, generator=g).to(torch.bfloat16)
+          for _ in range(n_sets)]
+    lens_dev = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    scale = 1.0 / math.sqrt(c["D"])
+
+    def step(i):
+        (kn, kp), (vn, vp) = sets[i % n_sets]
+        return ops.attention_packed(qs[i % n_sets], kn, kp, vn, vp, kc, vc, scale, False,
+                                    seq_lens=lens_dev)
+
+    steps = max(5, args.steps // 10)
+    ms, outs, _ = graph_timed(torch, step, steps, max(2, args.warmup // 4), dev)
+    if not torch.equal(outs[0], step(0)):
+        raise RuntimeError("config 2: graph replay differs from the eager call")
+    del sets, outs
+    _free(torch)
+    gbs = per_step / (ms * 1e-3) / 1e9
+    return {"workload": "cfg2 ragged decode: 32 seqs, T~U[2048,8192] (seed 1004), 16 q / 8 kv heads, "
+                        "d=256, K 4-bit / V 2-bit, dense 256x256 rotation, f32 norms",
+            "value": round(gbs, 2), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "us_per_step": round(ms * 1e3, 3), "sum_tokens": int(lens.sum()),
+            "bytes_per_step": per_step, "decode_tokens_per_s": round(c["B"] * 1e3 / ms, 1),
+            "steps": steps}
+
+
+def bench_prefill_append(torch, args, dev):
+    """Config 3: one 8192-token bf16 chunk appended to each of 36 layers.
+
+    Layers 0-3 keep model-dtype K/V (plain copy); layers 4-35 rotate by a dense
+    128x128 matrix on the matrix cores, quantize to 3 bits and pack.  Every
+    layer reads its own input tensors, so nothing is served from cache.
+    """
+    from kaplumba_amd import ops
+
+    c = CFG3
+    H, T, D, bits = c["Hkv"], c["T"], c["D"], c["bits"]
+    kc = ops.Codec(D, bits, 0, rotation="dense")
+    vc = ops.Codec(D, bits, 1, rotation="dense")
+    g = torch.Generator(device=dev).manual_seed(3000)
+    inputs = [_synth_kv(torch, g, (1, H, T, D), torch.bfloat16, dev) for _ in range(c["layers"])]
+    dst = []
+    for li in range(c["layers"]):
+        if li < c["plain_layers"]:
+            dst.append([torch.empty((1, H, T, D), dtype=torch.bfloat16, device=dev) for _ in range(2)])
+        else:
+            dst.append([(torch.empty((1, H, T, codec.packed_width), dtype=torch.uint32, device=dev),
+                         torch.empty((1, H, T), dtype=torch.float32, device=dev)) for codec in (kc, vc)])
+
+    def layer(li):
+        k, v = inputs[li]
+        if li < c["plain_layers"]:
+            ops.append_plain(k, dst[li][0], 0)
+            ops.append_plain(v, dst[li][1], 0)
+        else:
+            (kp, kn), (vp, vn) = dst[li]
+            ops.append_quantize(k, kc, kp, kn, 0)
+            ops.append_quantize(v, vc, vp, vn, 0)
+
+    def step(_i):
+        for li in range(c["layers"]):
+            layer(li)
+
+    n_q = c["layers"] - c["plain_layers"]
+
+    def step_quant(_i):
+        for li in range(c["plain_layers"], c["layers"]):
+            layer(li)
+
+    steps = max(3, args.steps // 40)
+    ms, _, _ = graph_timed(torch, step, steps, 2, dev)
+    ms_q, _, _ = graph_timed(torch, step_quant, steps, 2, dev)
+    del inputs, dst
+    _free(torch)
+    qbytes = quantize_bytes(H * T, D, bits, 2, 4)           # one K or V launch
+    pbytes = H * T * D * 2 * 2                              # plain layer tensor: read + write
+    total = n_q * 2 * qbytes + c["plain_layers"] * 2 * pbytes
+    launch_us = ms_q * 1e3 / (2 * n_q)
+    flops = 2.0 * H * T * D * D                             # u @ R^T per launch
+    return {"workload": "cfg3 prefill append: 36 layers x bf16 K,V [8,8192,128]; layers 0-3 stored "
+                        "unquantized, 4-35 dense 128x128 rotation (matrix cores) + 3-bit pack, f32 norms",
+            "value": round(total / (ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+            "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_per_step": round(ms * 1e3, 2), "bytes_per_step": total,
+            "prefill_tokens_per_s": round(T * 1e3 / ms, 1),
+            "dense_quantize": {"us_per_launch": round(launch_us, 3), "bytes_per_launch": qbytes,
+                               "GB/s": round(qbytes / (launch_us * 1e-6) / 1e9, 2),
+                               "rotation_tflops": round(flops / (launch_us * 1e-6) / 1e12, 1),
+                               "mfma_frac": round(3 * flops / (launch_us * 1e-6) / 1e12
+                                                  / MFMA_BF16_PEAK_TFLOPS, 4),
+                               "note": "rotation_tflops counts u@R^T once; the matrix cores run it "
+                                       "three times (bf16 pieces of R), which mfma_frac counts"},
+            "steps": steps}
+
+
+def bench_verify(torch, args, dev):
+    """Config 4: batch 4 x 4 causal drafts over 131072 + 4 tokens, K2/V1, plus fp16 K/V."""
+    from kaplumba_amd import ops
+
+    c = CFG4
+    B, H, T, D = c["B"], c["Hkv"], c["T"], c["D"]
+    kc, vc = ops.Codec(D, c["kb"], 0), ops.Codec(D, c["vb"], 1)
+    per_step = B * H * T * (4 * kc.packed_width + 4 * vc.packed_width + 8)
+    n_sets = max(2, math.ceil(args.rotate_mb * 1e6 / per_step))
+    g = torch.Generator(device=dev).manual_seed(4000)
+    sets = []
+    for _ in range(n_sets):
+        st = []
+        for codec, x in zip((kc, vc), _synth_kv(torch, g, (B, H, T, D), torch.float16, dev)):
+            pk = torch.empty((B, H, T, codec.packed_width), dtype=torch.uint32, device=dev)
+            nm = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+            ops.append_quantize(x, codec, pk, nm, 0)
+            st.append((nm, pk))
+            del x
+        sets.append(st)
+        _free(torch)
+    qs = [torch.randn(B, c["Hq"], c["L"], D, device=dev, generator=g).to(torch.bfloat16)
+          for _ in range(n_sets)]
+    scale = 1.0 / math.sqrt(D)
+
+    def step(i):
+        (kn, kp), (vn, vp) = sets[i % n_sets]
+        return ops.attention_packed(qs[i % n_sets], kn, kp, vn, vp, kc, vc, scale, True)
+
+    steps = max(5, args.steps // 10)
+    ms, outs, _ = graph_timed(torch, step, steps, max(2, args.warmup // 4), dev)
+    if not torch.equal(outs[0], step(0)):
+        raise RuntimeError("config 4: graph replay differs from the eager call")
+    del sets, outs
+    _free(torch)
+    # fp16-layer variant: the same shape over unquantized K/V
+    kv = _synth_kv(torch, g, (B, H, T, D), torch.float16, dev)
+    plain_bytes = 2 * B * H * T * D * 2
+
+    def step_plain(i):
+        return ops.attention_plain(qs[i % n_sets], kv[0], kv[1], scale, True)
+
+    steps_p = max(3, args.steps // 20)
+    ms_p, _, _ = graph_timed(torch, step_plain, steps_p, 2, dev)
+    del kv
+    _free(torch)
+    gbs = per_step / (ms * 1e-3) / 1e9
+    gbs_p = plain_bytes / (ms_p * 1e-3) / 1e9
+    return {"workload": "cfg4 verify: batch 4 x 4 causal drafts, 32 q / 8 kv heads, d=128, "
+                        "131076 tokens, K 2-bit / V 1-bit, Hadamard rotation, f32 norms",
+            "value": round(gbs, 2), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "us_per_step": round(ms * 1e3, 3), "bytes_per_step": per_step,
+            "verified_tokens_per_s": round(B * c["L"] * 1e3 / ms, 1), "steps": steps,
+            "fp16_layer": {"value": round(gbs_p, 2), "unit": "GB/s",
+                           "frac": round(gbs_p / HBM_PEAK_GBS, 4),
+                           "us_per_step": round(ms_p * 1e3, 3), "bytes_per_step": plain_bytes,
+                           "steps": steps_p}}
+
+
 def cpu_baseline(seconds_budget=12.0):
     """Numpy restatement of the reference's array-path attention (oracle), cfg1 shape."""
     import numpy as np
@@ -190,6 +391,8 @@ def main():
     ap.add_argument("--rotate-mb", type=float, default=600.0,
                     help="total size of distinct caches walked by successive steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-cfg1", action="store_true",
+                    help="skip the config 0/2/3/4 legs (the headline line only)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -201,7 +404,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     dec = bench_decode(torch, args, dev)
-    qnt = bench_quantize(torch, args, dev)
+    _free(torch)
+    qnt = None if args.only_cfg1 else bench_quantize(torch, args, dev)
+    _free(torch)
     value = dec["bytes"] / (dec["ms_per_step"] * 1e-3) / 1e9
     line = {
         "metric": "packed-KV decode attention GB/s (% HBM peak) @32k ctx 3-bit; quantize GB/s",
@@ -226,10 +431,15 @@ def main():
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "attention call: attn_mfma_kernel<128,3,3,4> + attn_merge_kernel<128>",
                      "kernel_us": round(dec["ms_per_step"] * 1e3, 3)},
-        "quantize": {"workload": "cfg0 append-quantize K+V f16 [1,8,4096,128] 3-bit",
-                     "value": round(qnt["bytes"] / (qnt["ms_per_step"] * 1e-3) / 1e9, 2),
-                     "unit": "GB/s", "step_us": round(qnt["ms_per_step"] * 1e3, 3)},
     }
+    if not args.only_cfg1:
+        line["quantize"] = {"workload": "cfg0 append-quantize K+V f16 [1,8,4096,128] 3-bit, "
+                                        "Hadamard rotation",
+                            "value": round(qnt["bytes"] / (qnt["ms_per_step"] * 1e-3) / 1e9, 2),
+                            "unit": "GB/s", "step_us": round(qnt["ms_per_step"] * 1e3, 3)}
+        line["cfg2"] = bench_ragged(torch, args, dev)
+        line["cfg3"] = bench_prefill_append(torch, args, dev)
+        line["cfg4"] = bench_verify(torch, args, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

@@ -1,0 +1,24 @@
+// Arguments shared by the append-time quantizers (Hadamard and dense rotation).
+#pragma once
+
+#include "tq_common.h"
+
+namespace tq {
+
+struct AppendArgs {
+  const void* x;
+  int64_t sb, sh, sl;  // element strides of x
+  int B, H, L;
+  const float* rot;    // Hadamard: signs (D); dense: R (D x D, row-major)
+  const float* mid;    // 2^bits - 1 midpoints
+  uint32_t* packed;
+  void* norms;
+  int norm_dtype;
+  int64_t cap, offset;
+  float scale;         // f32(1/sqrt(D)), Hadamard only
+};
+
+// Dense-rotation quantizer on the matrix cores (tq_append_dense.hip).
+int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
+
+}  // namespace tq

@@ -14,22 +14,9 @@
 //   * y = v * f32(1/sqrt(D)); idx = #{m : y > mid[m]} (strict compare);
 //   * a lane's 32 indices fill exactly `bits` consecutive words of the
 //     LSB-first stream, so packing is thread-local (no shared-word races).
-#include "tq_common.h"
+#include "tq_append.h"
 
 namespace tq {
-
-struct AppendArgs {
-  const void* x;
-  int64_t sb, sh, sl;  // element strides of x
-  int B, H, L;
-  const float* rot;    // signs (D)
-  const float* mid;    // 2^bits - 1 midpoints
-  uint32_t* packed;
-  void* norms;
-  int norm_dtype;
-  int64_t cap, offset;
-  float scale;         // f32(1/sqrt(D))
-};
 
 // Load 32 consecutive elements of dtype DT starting at p (16-byte aligned).
 template <int DT>
@@ -287,11 +274,6 @@ int launch_append_rht(int bits, int x_dtype, const AppendArgs& a, hipStream_t st
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
-
-// Implemented in tq_append_dense.hip (matrix-core rotation).
-namespace tq {
-int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
-}
 
 extern "C" int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
                                   int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,

@@ -1,9 +1,318 @@
-// Dense-rotation append (matrix cores).  Placeholder until the MFMA kernel lands.
-#include "tq_common.h"
+// Dense-rotation append on the matrix cores (gfx950, v_mfma_f32_32x32x16_bf16).
+//
+// Semantics: _TurboQuantMSECodec.quantize with the dense rotation
+// (turboquant_cache.py:4248-4254, _rotate_forward = u @ R^T at :4141-4144):
+//   n = ||x||_2 (f32), u = x / max(n, 1e-6), y = u @ R^T, idx_i = #{m : y_i > mid_m},
+// packed LSB-first like the Hadamard path.  The norm uses the Hadamard
+// kernel's reduction tree, so norms are bit-identical to it.
+//
+// Arithmetic.  The matrix cores compute y * max(n, eps) = x @ R^T: R is split
+// once per workgroup into three bf16 pieces R = R0 + R1 + R2 (each the
+// round-to-nearest-even bf16 of what the previous pieces leave; together they
+// carry R's full 24-bit significand), x enters as bf16 (exact for bf16 input;
+// f16 input is the exact sum of two bf16 pieces and f32 input the sum of three),
+// every piece product is exact and the sum runs in f32.  Products whose piece
+// orders add up to more than 2 are below f32 resolution and skipped.  Instead
+// of dividing, each coordinate is compared with mid_m * max(n, eps), computed
+// once per vector.  The result therefore differs from an f32 `u @ R^T` only in
+// the last bits of the sum, so an index can differ only where y lies within a
+// few f32 ulps of a midpoint (MLX's own f32 matmul order is not specified
+// either).
+//
+// Work split.  One workgroup = 8 waves x 32 vectors.  A wave computes
+// Y^T[coords][32 vectors] = R_slice (A, from LDS) x X^T (B, from HBM):
+//   * B lane (v = lane % 32, g = lane / 32) loads the D/2 consecutive elements
+//     [g*D/2, (g+1)*D/2) of vector v, which is exactly its B operand over all
+//     k-steps once the contraction index is permuted: MFMA k-slot 8g + j of
+//     k-step s stands for element g*D/2 + 8s + j (A uses the same permutation).
+//     These are also the elements whose squares the norm tree sums first.
+//   * A tile t of 32 rows holds R rows permuted so that, in the 32x32 output
+//     layout (lane l, register i = row 8(i/4) + 4(l/32) + i%4, column l%32),
+//     lane g of the pair of tiles (2p, 2p+1) ends up with the 32 consecutive
+//     coordinates c0 + 64p + 32g + [0, 32): packing is thread-local.
+//   * R pieces live in LDS in fragment order (one 16-byte slot per lane per
+//     tile, k-step and piece), so every A read is a conflict-free ds_read_b128.
+// For D = 256 the 256 coordinates are split over 4 workgroups of 64 (LDS
+// holds R pieces for 64 x 256); each of them reads the whole vector.
+#include "tq_append.h"
 
 namespace tq {
-struct AppendArgs;
-int launch_append_dense(const AppendArgs&, int dim, int bits, int, hipStream_t) {
-  return fail(TQ_ERR_UNSUPPORTED, "append: dense rotation (dim %d, bits %d) not built yet", dim, bits);
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kDenseThreads = 512;
+constexpr int kDenseWaves = kDenseThreads / kWave;
+
+template <int D>
+struct DenseShape {
+  static constexpr int CT = D == 128 ? 128 : 64;          // coordinates per workgroup
+  static constexpr int NSLICE = D / CT;                   // workgroups per vector tile
+  static constexpr int NT = CT / 32;                      // 32-row coordinate tiles
+  static constexpr int KS = D / 16;                       // k-steps
+  static constexpr int LE = D / 2;                        // x elements per lane
+  static constexpr int NRP = 3;                           // bf16 pieces of R
+  static constexpr int SLOTS = NRP * NT * KS * kWave;     // 16-byte A fragments
+  static constexpr int VPT = kDenseWaves * 32;            // vectors per workgroup tile
+  static_assert(NT % 2 == 0, "coordinate tiles come in pairs");
+};
+
+template <int XDT>
+struct XPieces {  // bf16 pieces whose sum is the input element exactly
+  static constexpr int N = XDT == TQ_DTYPE_BF16 ? 1 : (XDT == TQ_DTYPE_F16 ? 2 : 3);
+  static constexpr int ES = XDT == TQ_DTYPE_F32 ? 4 : 2;
+};
+
+__device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
+
+// Split f into NP bf16 pieces (round-to-nearest-even each, exact remainders).
+template <int NP>
+__device__ __forceinline__ void split_bf16(float f, uint16_t (&p)[NP]) {
+  float r = f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    p[i] = f32_to_bf16_bits(r);
+    r = __fsub_rn(r, bf16_bits_to_f32(p[i]));
+  }
+}
+
+// Element e of the lane's run of x, as f32.
+template <int XDT, int NX>
+__device__ __forceinline__ float x_elem(const u32x4_t (&xr)[NX], int e) {
+  if constexpr (XDT == TQ_DTYPE_F32) {
+    return __uint_as_float(xr[e >> 2][e & 3]);
+  } else {
+    const uint32_t w = xr[e >> 3][(e >> 1) & 3];
+    const uint16_t h = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+    return XDT == TQ_DTYPE_F16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+  }
+}
+
+template <int D, int BITS, int XDT>
+__global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs a) {
+  using S = DenseShape<D>;
+  using XP = XPieces<XDT>;
+  constexpr int NMID = (1 << BITS) - 1;
+  constexpr int PW = D * BITS / 32;
+  constexpr int NX = S::LE * XP::ES / 16;  // 16-byte loads per lane
+  __shared__ u32x4_t s_r[S::SLOTS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int vl = lane % 32;
+  const int g = lane / 32;
+  const int slice = blockIdx.x % S::NSLICE;
+  const int c0 = slice * S::CT;
+  const int64_t tile_stride = gridDim.x / S::NSLICE;
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+
+  // Input run of this lane for a given tile (zeros past the last vector).
+  auto load_x = [&](int64_t tile, u32x4_t (&xr)[NX], int64_t& row) {
+    const int64_t vec = tile * S::VPT + wave * 32 + vl;
+    row = -1;
+    if (vec < n_vec) {
+      const int l = static_cast<int>(vec % a.L);
+      const int64_t bh = vec / a.L;
+      const int h = static_cast<int>(bh % a.H);
+      const int b = static_cast<int>(bh / a.H);
+      const int64_t xoff = b * a.sb + h * a.sh + l * a.sl + g * S::LE;
+      const u32x4_t* src =
+          reinterpret_cast<const u32x4_t*>(static_cast<const char*>(a.x) + xoff * XP::ES);
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xr[i] = src[i];
+      row = (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l;
+    } else {
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xr[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+
+  int64_t tile = blockIdx.x / S::NSLICE;
+  u32x4_t xr[NX];
+  int64_t row;
+  load_x(tile, xr, row);  // in flight while R is split into LDS
+
+  // ---- R pieces -> LDS in A-fragment order
+  for (int f = tid; f < S::NT * S::KS * kWave; f += kDenseThreads) {
+    const int ln = f % kWave;
+    const int ks = (f / kWave) % S::KS;
+    const int t = f / (kWave * S::KS);
+    const int r = ln % 32;
+    const int coord = c0 + 64 * (t / 2) + 32 * ((r >> 2) & 1) + 16 * (t & 1) + 4 * (r >> 3) + (r & 3);
+    const float4* src =
+        reinterpret_cast<const float4*>(a.rot + static_cast<int64_t>(coord) * D + (ln / 32) * S::LE + 8 * ks);
+    const float4 v0 = src[0], v1 = src[1];
+    const float e[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t w[S::NRP][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint16_t lo[S::NRP], hi[S::NRP];
+      split_bf16<S::NRP>(e[2 * j], lo);
+      split_bf16<S::NRP>(e[2 * j + 1], hi);
+#pragma unroll
+      for (int p = 0; p < S::NRP; ++p) w[p][j] = lo[p] | (static_cast<uint32_t>(hi[p]) << 16);
+    }
+#pragma unroll
+    for (int p = 0; p < S::NRP; ++p)
+      s_r[(p * S::NT * S::KS) * kWave + f] = u32x4_t{w[p][0], w[p][1], w[p][2], w[p][3]};
+  }
+  float mid[NMID];
+#pragma unroll
+  for (int m = 0; m < NMID; ++m) mid[m] = a.mid[m];
+  __syncthreads();
+
+  for (; tile * S::VPT < n_vec; tile += tile_stride) {
+    // ---- norm: 32-element folds 16, 8, 4, 2, 1, groups pairwise, then the partner lane
+    constexpr int NG = S::LE / 32;
+    float gs[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      float s[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float u0 = x_elem<XDT, NX>(xr, 32 * q + i);
+        const float u1 = x_elem<XDT, NX>(xr, 32 * q + i + 16);
+        s[i] = __fadd_rn(__fmul_rn(u0, u0), __fmul_rn(u1, u1));
+      }
+#pragma unroll
+      for (int w = 8; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int i = 0; i < w; ++i) s[i] = __fadd_rn(s[i], s[i + w]);
+      }
+      gs[q] = s[0];
+    }
+#pragma unroll
+    for (int w = 1; w < NG; w <<= 1) {
+#pragma unroll
+      for (int q = 0; q < NG; q += 2 * w) gs[q] = __fadd_rn(gs[q], gs[q + w]);
+    }
+    const float ss = __fadd_rn(gs[0], __shfl_xor(gs[0], 32, kWave));
+    const float n = sqrt_rn(ss);
+    const float den = fmaxf(n, kNormEps);
+    float thr[NMID];
+#pragma unroll
+    for (int m = 0; m < NMID; ++m) thr[m] = __fmul_rn(mid[m], den);
+
+    // ---- x @ R^T for this slice's coordinates
+    f32x16_t acc[S::NT];
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) acc[t] = f32x16_t{};
+#pragma unroll
+    for (int ks = 0; ks < S::KS; ++ks) {
+      u32x4_t xb[XP::N];
+      if constexpr (XDT == TQ_DTYPE_BF16) {
+        xb[0] = xr[ks];
+      } else {
+        uint16_t pc[8][XP::N];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) split_bf16<XP::N>(x_elem<XDT, NX>(xr, 8 * ks + j), pc[j]);
+#pragma unroll
+        for (int p = 0; p < XP::N; ++p)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            xb[p][j] = pc[2 * j][p] | (static_cast<uint32_t>(pc[2 * j + 1][p]) << 16);
+      }
+      // smallest terms first
+#pragma unroll
+      for (int rp = S::NRP - 1; rp >= 0; --rp) {
+#pragma unroll
+        for (int xp = XP::N - 1; xp >= 0; --xp) {
+          if (rp + xp > 2) continue;
+#pragma unroll
+          for (int t = 0; t < S::NT; ++t)
+            acc[t] = mfma32(s_r[((rp * S::NT + t) * S::KS + ks) * kWave + lane], xb[xp], acc[t]);
+        }
+      }
+      // keep each k-step's fragment reads next to its products (hoisting all
+      // of them ahead of the first product would need 4 VGPRs per fragment)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- quantize against mid * max(n, eps), pack 32 coordinates per lane and pair
+    if (row >= 0) {
+      uint32_t* dst_row = a.packed + row * PW;
+#pragma unroll
+      for (int p = 0; p < S::NT / 2; ++p) {
+        uint32_t words[BITS];
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) words[w] = 0u;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+          const float y = acc[2 * p + e / 16][e % 16];
+          uint32_t idx = 0;
+#pragma unroll
+          for (int m = 0; m < NMID; ++m) idx += (y > thr[m]) ? 1u : 0u;
+          const int pos = e * BITS;
+          const int wi = pos >> 5;
+          const int sh = pos & 31;
+          words[wi] |= idx << sh;
+          if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
+        }
+        uint32_t* dst = dst_row + ((c0 + 64 * p + 32 * g) / 32) * BITS;
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) dst[w] = words[w];
+      }
+      if (slice == 0 && g == 0) {
+        if (a.norm_dtype == TQ_DTYPE_F16)
+          static_cast<uint16_t*>(a.norms)[row] = f32_to_f16_bits(n);
+        else
+          static_cast<float*>(a.norms)[row] = n;
+      }
+    }
+    if ((tile + tile_stride) * S::VPT < n_vec) load_x(tile + tile_stride, xr, row);
+  }
+}
+
+template <int D, int BITS>
+int launch_dense_bits(const AppendArgs& a, int x_dtype, hipStream_t st) {
+  using S = DenseShape<D>;
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  const int64_t tiles = (n_vec + S::VPT - 1) / S::VPT;
+  // One workgroup per CU fits next to the 96 KiB of R pieces; larger batches loop.
+  const int64_t per_slice = std::min<int64_t>(tiles, std::max(1, device_cu_count() / S::NSLICE));
+  const dim3 grid(static_cast<unsigned>(per_slice * S::NSLICE));
+  switch (x_dtype) {
+    case TQ_DTYPE_F32:
+      hipLaunchKernelGGL((append_dense_kernel<D, BITS, TQ_DTYPE_F32>), grid, dim3(kDenseThreads), 0, st, a);
+      break;
+    case TQ_DTYPE_F16:
+      hipLaunchKernelGGL((append_dense_kernel<D, BITS, TQ_DTYPE_F16>), grid, dim3(kDenseThreads), 0, st, a);
+      break;
+    default:
+      hipLaunchKernelGGL((append_dense_kernel<D, BITS, TQ_DTYPE_BF16>), grid, dim3(kDenseThreads), 0, st, a);
+      break;
+  }
+  return check_launch("append_dense_kernel");
+}
+
+template <int D>
+int launch_dense_dim(const AppendArgs& a, int bits, int x_dtype, hipStream_t st) {
+  switch (bits) {
+    case 1: return launch_dense_bits<D, 1>(a, x_dtype, st);
+    case 2: return launch_dense_bits<D, 2>(a, x_dtype, st);
+    case 3: return launch_dense_bits<D, 3>(a, x_dtype, st);
+    case 4: return launch_dense_bits<D, 4>(a, x_dtype, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "append: bits %d not in 1..4", bits);
+}
+
+}  // namespace
+
+int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(a.rot) & 15u) != 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: dense rotation matrix must be 16-byte aligned");
+  switch (dim) {
+    case 64: return launch_dense_dim<64>(a, bits, x_dtype, st);
+    case 128: return launch_dense_dim<128>(a, bits, x_dtype, st);
+    case 256: return launch_dense_dim<256>(a, bits, x_dtype, st);
+  }
+  return fail(TQ_ERR_UNSUPPORTED, "append: dense rotation needs dim in {64, 128, 256}, got %d", dim);
+}
+
 }  // namespace tq

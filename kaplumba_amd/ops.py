@@ -73,7 +73,7 @@ class Codec:
         d = self._dev.get(key)
         if d is None:
             d = {
-                "rot": torch.from_numpy(np.ascontiguousarray(self.rot_host)).to(device),
+                "rot": torch.from_numpy(np.array(self.rot_host, dtype=np.float32, order="C")).to(device),
                 "codebook": torch.from_numpy(self.codebook.copy()).to(device),
                 "midpoints": torch.from_numpy(
                     self.midpoints.copy() if self.midpoints.size else np.zeros(1, np.float32)).to(device),
