@@ -391,8 +391,9 @@ def main():
     ap.add_argument("--rotate-mb", type=float, default=600.0,
                     help="total size of distinct caches walked by successive steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only-cfg1", action="store_true",
-                    help="skip the config 0/2/3/4 legs (the headline line only)")
+    ap.add_argument("--legs", default="cfg0,cfg2,cfg3,cfg4",
+                    help="comma-separated extra legs to run after the cfg1 headline "
+                         "(cfg0, cfg2, cfg3, cfg4; empty for the headline only)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -405,8 +406,10 @@ def main():
     dev = torch.device("cuda", 0)
     dec = bench_decode(torch, args, dev)
     _free(torch)
-    qnt = None if args.only_cfg1 else bench_quantize(torch, args, dev)
-    _free(torch)
+    legs = {x.strip() for x in args.legs.split(",") if x.strip()}
+    unknown = legs - {"cfg0", "cfg2", "cfg3", "cfg4"}
+    if unknown:
+        ap.error(f"unknown legs: {sorted(unknown)}")
     value = dec["bytes"] / (dec["ms_per_step"] * 1e-3) / 1e9
     line = {
         "metric": "packed-KV decode attention GB/s (% HBM peak) @32k ctx 3-bit; quantize GB/s",
@@ -432,13 +435,18 @@ def main():
                      "kernel": "attention call: attn_mfma_kernel<128,3,3,4> + attn_merge_kernel<128>",
                      "kernel_us": round(dec["ms_per_step"] * 1e3, 3)},
     }
-    if not args.only_cfg1:
+    if "cfg0" in legs:
+        qnt = bench_quantize(torch, args, dev)
+        _free(torch)
         line["quantize"] = {"workload": "cfg0 append-quantize K+V f16 [1,8,4096,128] 3-bit, "
                                         "Hadamard rotation",
                             "value": round(qnt["bytes"] / (qnt["ms_per_step"] * 1e-3) / 1e9, 2),
                             "unit": "GB/s", "step_us": round(qnt["ms_per_step"] * 1e3, 3)}
+    if "cfg2" in legs:
         line["cfg2"] = bench_ragged(torch, args, dev)
+    if "cfg3" in legs:
         line["cfg3"] = bench_prefill_append(torch, args, dev)
+    if "cfg4" in legs:
         line["cfg4"] = bench_verify(torch, args, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()

@@ -8,28 +8,91 @@
 namespace tq {
 
 // ------------------------------------------------------------------ qprep ---
-// Dense rotation only: one block per query row (b, h, l), D threads.
+// Dense rotation only:
 //   q_s = round_qdtype(q * scale_q)     (MLX weak-scalar multiply, :5802)
 //   q_rot = q_s @ R_K^T                 (turboquant_cache.py:4144)
-// Doing this once per row (instead of once per workgroup) keeps the D x D
-// matrix from being re-read by every split.
-template <int QDT>
-__global__ __launch_bounds__(256) void qprep_kernel(AttnParams p) {
-  __shared__ float y[256];
-  const int64_t row = blockIdx.x;  // (b*Hq + h)*L + l
-  const int l = static_cast<int>(row % p.L);
-  const int64_t bh = row / p.L;
-  const int h = static_cast<int>(bh % p.Hq);
-  const int b = static_cast<int>(bh / p.Hq);
-  const int i = threadIdx.x;
-  const int D = p.D;
-  const float qv = load_elem<QDT>(p.q, b * p.q_sb + h * p.q_sh + l * p.q_sl + i);
-  y[i] = round_to<QDT>(qv * p.scale_q);
+// Block (row block, coordinate block) computes q_rot[r][i] for kQprepRows
+// query rows and 64 coordinates i.  Thread (i, quarter jq) holds the quarter
+// jq of row i of R_K in registers and forms partial dot products with every
+// query row of the block (the rows are LDS broadcasts: a wave shares jq);
+// the four partials of (r, i) fold through LDS.  R_K crosses L2 once per
+// kQprepRows query rows.
+constexpr int kQprepRows = 16;
+constexpr int kQprepThreads = 256;
+
+template <int QDT, int D>
+__global__ __launch_bounds__(kQprepThreads) void qprep_kernel(AttnParams p, int64_t n_rows) {
+  constexpr int JL = D / 4;  // coordinates j per thread
+  __shared__ float4 s_q4[kQprepRows][D / 4];
+  __shared__ float s_part[4][kQprepRows][64];
+  const int tid = threadIdx.x;
+  const int il = tid % 64;
+  const int jq = tid / 64;
+  const int i = blockIdx.y * 64 + il;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kQprepRows;
+  float4 rv[JL / 4];
+  const float4* src = reinterpret_cast<const float4*>(p.krot + static_cast<int64_t>(i) * D + jq * JL);
+#pragma unroll
+  for (int m = 0; m < JL / 4; ++m) rv[m] = src[m];
+  // query rows: thread (row r, segment) loads D/16 consecutive elements with
+  // independent loads (one index computation per thread)
+  static_assert(kQprepThreads == 16 * kQprepRows, "one segment per thread");
+  {
+    constexpr int SEG = D / 16;
+    float* s_q = reinterpret_cast<float*>(s_q4);
+    const int r = tid / 16;
+    const int j0 = (tid % 16) * SEG;
+    const int64_t row = row0 + r;  // (b*Hq + h)*L + l
+    float v[SEG];
+    if (row < n_rows) {
+      const int l = static_cast<int>(row % p.L);
+      const int64_t bh = row / p.L;
+      const int h = static_cast<int>(bh % p.Hq);
+      const int b = static_cast<int>(bh / p.Hq);
+      const int64_t base = b * p.q_sb + h * p.q_sh + l * p.q_sl + j0;
+#pragma unroll
+      for (int e = 0; e < SEG; ++e) v[e] = load_elem<QDT>(p.q, base + e);
+#pragma unroll
+      for (int e = 0; e < SEG; ++e) v[e] = round_to<QDT>(v[e] * p.scale_q);
+    } else {
+#pragma unroll
+      for (int e = 0; e < SEG; ++e) v[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < SEG; ++e) s_q[r * D + j0 + e] = v[e];
+  }
   __syncthreads();
-  const float* Rrow = p.krot + static_cast<int64_t>(i) * D;  // y_i = sum_j q_j R[i][j]
-  float acc = 0.f;
-  for (int j = 0; j < D; ++j) acc = fmaf(y[j], Rrow[j], acc);
-  p.qrot[row * D + i] = acc;
+#pragma unroll
+  for (int r = 0; r < kQprepRows; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int m = 0; m < JL / 4; ++m) {
+      const float4 q = s_q4[r][jq * (JL / 4) + m];
+      acc = fmaf(q.x, rv[m].x, acc);
+      acc = fmaf(q.y, rv[m].y, acc);
+      acc = fmaf(q.z, rv[m].z, acc);
+      acc = fmaf(q.w, rv[m].w, acc);
+    }
+    s_part[jq][r][il] = acc;
+  }
+  __syncthreads();
+  for (int o = tid; o < kQprepRows * 64; o += kQprepThreads) {
+    const int r = o / 64;
+    const int c = o % 64;
+    if (row0 + r < n_rows)
+      p.qrot[(row0 + r) * D + blockIdx.y * 64 + c] =
+          (s_part[0][r][c] + s_part[1][r][c]) + (s_part[2][r][c] + s_part[3][r][c]);
+  }
+}
+
+template <int D>
+void launch_qprep(const AttnParams& p, int q_dtype, int64_t rows, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((rows + kQprepRows - 1) / kQprepRows), D / 64);
+  switch (q_dtype) {
+    case TQ_DTYPE_F32: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_F32, D>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
+    case TQ_DTYPE_F16: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_F16, D>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
+    default: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_BF16, D>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
+  }
 }
 
 // ------------------------------------------------------------- planning ---
@@ -204,11 +267,10 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   p.rscale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
   int rc = TQ_OK;
   if (kv_kind == TQ_KV_PACKED && rot_kind == TQ_ROT_DENSE) {
-    const dim3 rgrid(static_cast<unsigned>(rows));
-    switch (q_dtype) {
-      case TQ_DTYPE_F32: hipLaunchKernelGGL(qprep_kernel<TQ_DTYPE_F32>, rgrid, dim3(dim), 0, st, p); break;
-      case TQ_DTYPE_F16: hipLaunchKernelGGL(qprep_kernel<TQ_DTYPE_F16>, rgrid, dim3(dim), 0, st, p); break;
-      default: hipLaunchKernelGGL(qprep_kernel<TQ_DTYPE_BF16>, rgrid, dim3(dim), 0, st, p); break;
+    switch (dim) {
+      case 64: launch_qprep<64>(p, q_dtype, rows, st); break;
+      case 128: launch_qprep<128>(p, q_dtype, rows, st); break;
+      default: launch_qprep<256>(p, q_dtype, rows, st); break;
     }
     rc = check_launch("qprep_kernel");
     if (rc) return rc;
@@ -221,7 +283,10 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   }
   if (rc || kv_kind != TQ_KV_PACKED || sp.n_splits == 1) return rc;
   // packed caches: the splits' partials are merged by a second kernel
-  const dim3 mgrid(static_cast<unsigned>(sp.nq), static_cast<unsigned>(Hkv * sp.n_rg), static_cast<unsigned>(B));
+  // one workgroup per query row; for the dense rotation one per 64 output
+  // columns of a row group (R_V^-1 is read once per row group)
+  const unsigned mx = rot_kind == TQ_ROT_DENSE ? static_cast<unsigned>(dim / 64) : static_cast<unsigned>(sp.nq);
+  const dim3 mgrid(mx, static_cast<unsigned>(Hkv * sp.n_rg), static_cast<unsigned>(B));
   switch (dim) {
     case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mgrid, dim3(kMergeThreads), 0, st, p); break;
     case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mgrid, dim3(kMergeThreads), 0, st, p); break;

@@ -137,23 +137,22 @@ struct MfmaShape {
   static constexpr int VRAW = VB == 3 ? 2 : 1;  // a 3-bit segment can cross a word
   static constexpr int PWV = D * VB / 32;
   static constexpr int VKEYS = 1 << (2 * VB);
-  static constexpr int REPV = VKEYS <= 64 ? 64 : 16;
+  static constexpr int REPV = VKEYS <= 64 ? 64 : 16;  // (hi pair, lo pair) entries, like keys
   // LDS layout (bytes)
   // Pair tables sit on aligned blocks: an entry's byte address is
   // base | key << LOG_STRIDE with the key bits clear in base (replica
   // offset of the lane + block start).
   static constexpr int LOGSK = REPK == 64 ? 9 : 6;  // log2(REPK * 8): (hi pair, lo pair) entries
-  static constexpr int LOGSV = REPV == 64 ? 8 : 6;  // log2(REPV * 4): f16 pair entries
+  static constexpr int LOGSV = REPV == 64 ? 9 : 7;  // log2(REPV * 8): (hi pair, lo pair) entries
   static constexpr int LUTK_BYTES = KKEYS * REPK * 8;
-  static constexpr int LUTV_BYTES = VKEYS * REPV * 4;
+  static constexpr int LUTV_BYTES = VKEYS * REPV * 8;
   static constexpr int LUTK_OFF = 0;      // keys: 32 KiB block
-  static constexpr int LUTV_OFF = 32768;  // values: 16 KiB block
+  static constexpr int LUTV_OFF = 32768;  // values: 32 KiB block
   static constexpr int QSTRIDE = D + 4;   // padded rows: the 16 rows read apart land on distinct banks
-  static constexpr int Q_OFF = 49152;     // [NQ][QSTRIDE] f32 rotated queries
+  static constexpr int Q_OFF = 65536;     // [NQ][QSTRIDE] f32 rotated queries
   static constexpr int QS_OFF = Q_OFF + NQ * QSTRIDE * 4;  // [NQ] f32 max |q_rot| per row
   static constexpr int W_OFF = QS_OFF + 64;            // [NW][16][32] f16 weights
-  static constexpr int SERR_OFF = W_OFF + NW * 16 * SUB * 2;  // [4] f32 + [4] int scale search
-  static constexpr int CO_OFF = SERR_OFF + 64;       // [NW][NQ][D] f32 wave outputs
+  static constexpr int CO_OFF = W_OFF + NW * 16 * SUB * 2;  // [NW][NQ][D] f32 wave outputs
   static constexpr int CM_OFF = CO_OFF + NW * NQ * D * 4;
   static constexpr int CL_OFF = CM_OFF + NW * NQ * 4;
   static constexpr int O_OFF = CL_OFF + NW * NQ * 4;  // [NQ][D] combined rows
@@ -164,7 +163,8 @@ struct MfmaShape {
   static constexpr int QPL = D / kWave;           // query elements per lane and row
   static_assert(D % 64 == 0, "head dim");
   static_assert(CPL % SEGC == 0, "value segments");
-  static_assert(LUTK_BYTES <= 32768 && LUTV_BYTES <= 16384, "pair table blocks");
+  static_assert(LUTK_BYTES <= 32768 && LUTV_BYTES <= 32768, "pair table blocks");
+  static_assert(BYTES <= 160 * 1024, "LDS per workgroup");
 };
 
 // LDS barrier that orders only LDS traffic: unlike __syncthreads it does not
@@ -266,8 +266,6 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   float* s_q = reinterpret_cast<float*>(lds + S::Q_OFF);
   float* s_qs = reinterpret_cast<float*>(lds + S::QS_OFF);
   uint16_t* s_w = reinterpret_cast<uint16_t*>(lds + S::W_OFF);
-  float* s_serr = reinterpret_cast<float*>(lds + S::SERR_OFF);
-  int* s_sidx = reinterpret_cast<int*>(lds + S::SERR_OFF + 32);
   float* s_co = reinterpret_cast<float*>(lds + S::CO_OFF);
   float* s_cm = reinterpret_cast<float*>(lds + S::CM_OFF);
   float* s_cl = reinterpret_cast<float*>(lds + S::CL_OFF);
@@ -331,7 +329,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
     vsh[k] = bit & 31;
   }
   const uint32_t lutk_lane = S::LUTK_OFF + (lane % REPK) * 8;  // byte address of the lane's replica
-  const uint32_t lutv_lane = S::LUTV_OFF + (lane % REPV) * 4;
+  const uint32_t lutv_lane = S::LUTV_OFF + (lane % REPV) * 8;
   uint32_t kmask = (S::KKEYS - 1u) << S::LOGSK;  // table key masks in SGPRs
   uint32_t vmask = (S::VKEYS - 1u) << S::LOGSV;
   asm volatile("" : "+s"(kmask), "+s"(vmask));
@@ -425,54 +423,6 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
 #pragma unroll
   for (int i = 0; i < (1 << VB); ++i) vmax = fmaxf(vmax, fabsf(cvb[i]));
 
-  // value codebook scale: candidate s_i = (0.5 + i/512) / max|c| for threads
-  // i < 256; the worst relative f16 error over the entries, argmin with the
-  // smallest index on ties
-  if (tid < 256) {
-    const float sc = vmax > 0.f ? (0.5f + tid * (1.f / 512.f)) / vmax : 1.f;
-    float err = 0.f;
-#pragma unroll
-    for (int j = 0; j < (1 << VB); ++j) {
-      const float v = cvb[j] * sc;
-      if (v != 0.f)
-        err = fmaxf(err, fabsf(static_cast<float>(static_cast<_Float16>(v)) - v) *
-                             __builtin_amdgcn_rcpf(fabsf(v)));
-    }
-    // argmin (smallest index on ties) over the 16 lanes of each row by DPP
-    // rotations, then over the four rows by lane reads
-    int idx = tid;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float oe;
-      int oi;
-      switch (k) {
-        case 0: oe = row_ror<8>(err); oi = __builtin_bit_cast(int, row_ror<8>(__builtin_bit_cast(float, idx))); break;
-        case 1: oe = row_ror<4>(err); oi = __builtin_bit_cast(int, row_ror<4>(__builtin_bit_cast(float, idx))); break;
-        case 2: oe = row_ror<2>(err); oi = __builtin_bit_cast(int, row_ror<2>(__builtin_bit_cast(float, idx))); break;
-        default: oe = row_ror<1>(err); oi = __builtin_bit_cast(int, row_ror<1>(__builtin_bit_cast(float, idx))); break;
-      }
-      if (oe < err || (oe == err && oi < idx)) {
-        err = oe;
-        idx = oi;
-      }
-    }
-    float be = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, err), 0));
-    int bi = __builtin_amdgcn_readlane(idx, 0);
-#pragma unroll
-    for (int r = 1; r < 4; ++r) {
-      const float e2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, err), 16 * r));
-      const int i2 = __builtin_amdgcn_readlane(idx, 16 * r);
-      if (e2 < be || (e2 == be && i2 < bi)) {
-        be = e2;
-        bi = i2;
-      }
-    }
-    if (lane == 0) {
-      s_serr[wave] = be;
-      s_sidx[wave] = bi;
-    }
-  }
-
   // query rows: wave w rotates rows w, w + NW, ... in its own LDS rows
   //   q_s = round_qdtype(q * scale_q) * s_K, Hadamard butterflies, * 1/sqrt(D)
   //   (dense: the rows were rotated by qprep_kernel), then the hi/lo scale.
@@ -522,21 +472,12 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   }
   lds_barrier();
 
-  // pair tables: keys (hi pair, lo pair) at a power-of-two scale, values f16
-  // at the searched scale
+  // pair tables: keys and values as (hi pair, lo pair) f16 at power-of-two
+  // scales, so an entry carries ~22 significant bits (a single f16 would leave
+  // a per-entry rounding error that every token with that index repeats, i.e.
+  // a bias that does not average out over the context)
   const float sk = f16_split_scale(kmax);
-  float cbs_v;
-  {
-    float be = s_serr[0];
-    int bi = s_sidx[0];
-#pragma unroll
-    for (int w = 1; w < 4; ++w)
-      if (s_serr[w] < be || (s_serr[w] == be && s_sidx[w] < bi)) {
-        be = s_serr[w];
-        bi = s_sidx[w];
-      }
-    cbs_v = vmax > 0.f ? (0.5f + bi * (1.f / 512.f)) / vmax : 1.f;
-  }
+  const float cbs_v = f16_split_scale(vmax);
   {
     // Thread t computes the entry of key t % KEYS once and stores it in the
     // replicas (s + key) % REP for its slots s = t / KEYS, t / KEYS + NT / KEYS,
@@ -553,11 +494,13 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
       for (int sl = tid / S::KKEYS; sl < REPK; sl += NT / S::KKEYS)
         lk[key * REPK + (sl + key) % REPK] = ent;
     }
-    uint32_t* lv = reinterpret_cast<uint32_t*>(lds + S::LUTV_OFF);
+    uint2* lv = reinterpret_cast<uint2*>(lds + S::LUTV_OFF);
     {
       const int key = tid % S::VKEYS;
-      const uint32_t ent =
-          f16_bits(cvb[key & ((1 << VB) - 1)] * cbs_v) | (f16_bits(cvb[key >> VB] * cbs_v) << 16);
+      uint32_t h0, l0, h1, l1;
+      split_f16(cvb[key & ((1 << VB) - 1)] * cbs_v, h0, l0);
+      split_f16(cvb[key >> VB] * cbs_v, h1, l1);
+      const uint2 ent = make_uint2(h0 | (h1 << 16), l0 | (l1 << 16));
       for (int sl = tid / S::VKEYS; sl < REPV; sl += NT / S::VKEYS)
         lv[key * REPV + (sl + key) % REPV] = ent;
     }
@@ -764,13 +707,16 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
     for (int c = 0; c < CPL; ++c) {
       const int k = c / SEGC;
       const int cc = c % SEGC;
-      u32x4_t bv;
+      u32x4_t bh, bl;
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
         const uint32_t z[1] = {(cc & 1) ? zh[e2][k] : zl[e2][k]};
-        bv[e2] = lds_at<uint32_t>(lds, key_addr<2 * VB, S::LOGSV>(z, (cc >> 1) * 2 * VB, lutv_lane, vmask));
+        const uint2 v = lds_at<uint2>(lds, key_addr<2 * VB, S::LOGSV>(z, (cc >> 1) * 2 * VB, lutv_lane, vmask));
+        bh[e2] = v.x;
+        bl[e2] = v.y;
       }
-      O[c] = mfma_f16(A, bv, O[c]);
+      O[c] = mfma_f16(A, bl, O[c]);
+      O[c] = mfma_f16(A, bh, O[c]);
     }
   };
 

@@ -4,11 +4,15 @@
 // the unnormalised o[NQ][D] (already back in the unrotated basis for the
 // Hadamard rotation) and (m, l) per row with plain stores; kernel-boundary
 // ordering on the stream makes them visible here, so no atomics, counters or
-// cache-bypassing accesses are needed.  One workgroup merges one query row:
-// thread (float4 column c, split group sg) folds the splits sg, sg + SG, ...
-// by log-sum-exp, the split groups fold through LDS, and the row is
-// normalised by 1/max(l, 1e-6), rotated back by R_V^-1 for the dense
-// rotation, and stored in the query dtype.
+// cache-bypassing accesses are needed.  Thread (float4 column c, split group
+// sg) folds the splits sg, sg + SG, ... of a row by log-sum-exp, the split
+// groups fold through LDS, and the row is normalised by 1/max(l, 1e-6).
+//   Hadamard: grid.x = rows per group, one row per workgroup, stored directly.
+//   Dense: grid.x = D / 64 column blocks per row group.  Every block merges
+//   all rows of the group into LDS (the partials are small), then computes
+//   its 64 output columns of y @ R_V for all rows at once: 4 thread groups
+//   each sum a quarter of the k range with 16 loads of R_V in flight, so the
+//   D x D matrix is read once per row group, spread over D / 64 workgroups.
 // Semantics: quantized_attention's final o / max(l, eps), turboquant_cache.py:5190-5203.
 #pragma once
 
@@ -23,105 +27,133 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p)
   constexpr int C4 = D / 4;
   constexpr int SG = kMergeThreads / C4;  // split groups
   constexpr int BATCH = 8;                 // splits per thread per round trip
+  constexpr int MAXR = D >= 256 ? 4 : 16;  // rows per group (the partial kernel's NQ bound)
   static_assert(kMergeThreads % C4 == 0, "merge mapping");
   __shared__ float4 s_po[SG][C4];
   __shared__ float s_pm[SG], s_pl[SG];
-  __shared__ float s_y[D];
+  __shared__ float s_y[MAXR * D];
+  __shared__ float s_part[4][MAXR][64];
 
   const int tid = threadIdx.x;
-  const int j = blockIdx.x;  // row inside the row group
   const int gk = blockIdx.y / p.n_rg;
   const int rg = blockIdx.y % p.n_rg;
   const int b = blockIdx.z;
   RowSet rs;
   rs.init(p, b, gk, rg, p.nq);
-  if (!rs.valid(j)) return;
   int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
   if (Tb > p.T) Tb = p.T;
   const int nvalid = Tb > 0 ? static_cast<int>((Tb + p.chunk - 1) / p.chunk) : 0;
-  if (nvalid <= 1) return;  // the partial kernel wrote this row itself
+  if (nvalid <= 1) return;  // the partial kernel wrote these rows itself
+  const bool dense = p.rot_kind == TQ_ROT_DENSE;
 
   const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;
   const float* po_g = p.po + grp * static_cast<int64_t>(p.n_splits) * p.nq * D;
   const float* pml_g = p.pml + grp * static_cast<int64_t>(p.n_splits) * p.nq * 2;
   const int c = tid % C4;
   const int sg = tid / C4;
-  float M = -INFINITY, L = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp0 = sg; sp0 < nvalid; sp0 += SG * BATCH) {
-    float2 ml[BATCH];
-    float4 oo[BATCH];
+  const int j0 = dense ? 0 : static_cast<int>(blockIdx.x);
+  const int jstep = dense ? 1 : p.nq;
+  for (int j = j0; j < p.nq; j += jstep) {
+    if (!rs.valid(j)) break;  // valid rows are a prefix of the group
+    float M = -INFINITY, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int sp0 = sg; sp0 < nvalid; sp0 += SG * BATCH) {
+      float2 ml[BATCH];
+      float4 oo[BATCH];
 #pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const int sp = sp0 + u * SG;
-      if (sp < nvalid) {
-        const int64_t r = static_cast<int64_t>(sp) * p.nq + j;
-        ml[u] = reinterpret_cast<const float2*>(pml_g)[r];
-        oo[u] = reinterpret_cast<const float4*>(po_g + r * D)[c];
-      } else {
-        ml[u] = make_float2(-INFINITY, 0.f);
-        oo[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int u = 0; u < BATCH; ++u) {
+        const int sp = sp0 + u * SG;
+        if (sp < nvalid) {
+          const int64_t r = static_cast<int64_t>(sp) * p.nq + j;
+          ml[u] = reinterpret_cast<const float2*>(pml_g)[r];
+          oo[u] = reinterpret_cast<const float4*>(po_g + r * D)[c];
+        } else {
+          ml[u] = make_float2(-INFINITY, 0.f);
+          oo[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      float bm = M;
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) bm = fmaxf(bm, ml[u].x);
+      const float r0 = (M == -INFINITY) ? 0.f : __expf(M - bm);
+      L *= r0;
+      acc.x *= r0;
+      acc.y *= r0;
+      acc.z *= r0;
+      acc.w *= r0;
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const float sc = (ml[u].x == -INFINITY) ? 0.f : __expf(ml[u].x - bm);
+        L = fmaf(sc, ml[u].y, L);
+        acc.x = fmaf(sc, oo[u].x, acc.x);
+        acc.y = fmaf(sc, oo[u].y, acc.y);
+        acc.z = fmaf(sc, oo[u].z, acc.z);
+        acc.w = fmaf(sc, oo[u].w, acc.w);
+      }
+      M = bm;
+    }
+    s_po[sg][c] = acc;
+    if (c == 0) {
+      s_pm[sg] = M;
+      s_pl[sg] = L;
+    }
+    __syncthreads();
+    if (tid < C4) {
+      float Mt = -INFINITY;
+#pragma unroll
+      for (int g2 = 0; g2 < SG; ++g2) Mt = fmaxf(Mt, s_pm[g2]);
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+      float lt = 0.f;
+#pragma unroll
+      for (int g2 = 0; g2 < SG; ++g2) {
+        const float sc = (s_pm[g2] == -INFINITY) ? 0.f : __expf(s_pm[g2] - Mt);
+        lt = fmaf(sc, s_pl[g2], lt);
+        a.x = fmaf(sc, s_po[g2][tid].x, a.x);
+        a.y = fmaf(sc, s_po[g2][tid].y, a.y);
+        a.z = fmaf(sc, s_po[g2][tid].z, a.z);
+        a.w = fmaf(sc, s_po[g2][tid].w, a.w);
+      }
+      const float den = fmaxf(lt, kNormEps);
+      const float v[4] = {a.x / den, a.y / den, a.z / den, a.w / den};
+      const int64_t qo = rs.qoff(j) * D;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (dense)
+          s_y[j * D + 4 * tid + e] = v[e];
+        else
+          store_out(p.out, p.q_dtype, qo + 4 * tid + e, v[e]);
       }
     }
-    float bm = M;
-#pragma unroll
-    for (int u = 0; u < BATCH; ++u) bm = fmaxf(bm, ml[u].x);
-    const float r0 = (M == -INFINITY) ? 0.f : __expf(M - bm);
-    L *= r0;
-    acc.x *= r0;
-    acc.y *= r0;
-    acc.z *= r0;
-    acc.w *= r0;
-#pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const float sc = (ml[u].x == -INFINITY) ? 0.f : __expf(ml[u].x - bm);
-      L = fmaf(sc, ml[u].y, L);
-      acc.x = fmaf(sc, oo[u].x, acc.x);
-      acc.y = fmaf(sc, oo[u].y, acc.y);
-      acc.z = fmaf(sc, oo[u].z, acc.z);
-      acc.w = fmaf(sc, oo[u].w, acc.w);
-    }
-    M = bm;
-  }
-  s_po[sg][c] = acc;
-  if (c == 0) {
-    s_pm[sg] = M;
-    s_pl[sg] = L;
-  }
-  __syncthreads();
-  const bool dense = p.rot_kind == TQ_ROT_DENSE;
-  const int64_t qo = rs.qoff(j) * D;
-  if (tid < C4) {
-    float Mt = -INFINITY;
-#pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) Mt = fmaxf(Mt, s_pm[g2]);
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    float lt = 0.f;
-#pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) {
-      const float sc = (s_pm[g2] == -INFINITY) ? 0.f : __expf(s_pm[g2] - Mt);
-      lt = fmaf(sc, s_pl[g2], lt);
-      a.x = fmaf(sc, s_po[g2][tid].x, a.x);
-      a.y = fmaf(sc, s_po[g2][tid].y, a.y);
-      a.z = fmaf(sc, s_po[g2][tid].z, a.z);
-      a.w = fmaf(sc, s_po[g2][tid].w, a.w);
-    }
-    const float den = fmaxf(lt, kNormEps);
-    const float v[4] = {a.x / den, a.y / den, a.z / den, a.w / den};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (dense)
-        s_y[4 * tid + e] = v[e];
-      else
-        store_out(p.out, p.q_dtype, qo + 4 * tid + e, v[e]);
-    }
+    __syncthreads();  // s_po / s_pm are reused by the next row
   }
   if (!dense) return;
+  // x_d = sum_k y_k R[k][d] for every valid row, columns d of this block
+  int nrows = 0;
+  while (nrows < p.nq && nrows < MAXR && rs.valid(nrows)) ++nrows;
+  constexpr int KQ = D / 4;  // k range of one thread group
+  const int col = tid % 64;
+  const int kq = tid / 64;
+  const int d = static_cast<int>(blockIdx.x) * 64 + col;
+  float a2[MAXR];
+#pragma unroll
+  for (int j = 0; j < MAXR; ++j) a2[j] = 0.f;
+  for (int k0 = kq * KQ; k0 < (kq + 1) * KQ; k0 += 16) {
+    float r[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) r[u] = p.vrot[static_cast<int64_t>(k0 + u) * D + d];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+#pragma unroll
+      for (int j = 0; j < MAXR; ++j) a2[j] = fmaf(s_y[j * D + k0 + u], r[u], a2[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < MAXR; ++j) s_part[kq][j][col] = a2[j];
   __syncthreads();
-  for (int d = tid; d < D; d += kMergeThreads) {  // x_d = sum_k y_k R[k][d]
-    float a2 = 0.f;
-    for (int k2 = 0; k2 < D; ++k2) a2 = fmaf(s_y[k2], p.vrot[static_cast<int64_t>(k2) * D + d], a2);
-    store_out(p.out, p.q_dtype, qo + d, a2);
+  if (tid < 64) {
+    for (int j = 0; j < nrows; ++j) {
+      const float x = (s_part[0][j][tid] + s_part[1][j][tid]) + (s_part[2][j][tid] + s_part[3][j][tid]);
+      store_out(p.out, p.q_dtype, rs.qoff(j) * D + d, x);
+    }
   }
 }
 

@@ -154,6 +154,17 @@ def test_ragged_batch_dense_d256(device):
     run_case(device, 77, 5, 16, 8, 1, 1700, 256, 4, 2, rot="dense", lengths=lengths)
 
 
+@pytest.mark.parametrize("d,Hq,Hkv,L,T", [
+    (64, 8, 2, 1, 3000),     # 4-row groups, many splits
+    (128, 32, 8, 4, 2500),   # 16-row groups (GQA 4 x 4 drafts), causal
+    (128, 8, 8, 1, 700),     # MHA, one row per group
+    (256, 8, 2, 3, 2100),    # three 4-row groups per kv head, causal
+])
+def test_dense_rotation_shapes(device, d, Hq, Hkv, L, T):
+    """Dense R_K / R_V: the query rotation and the merge's R_V^-1 over whole row groups."""
+    run_case(device, 40 + d + L, 2, Hq, Hkv, L, T, d, 3, 2, rot="dense")
+
+
 def test_ragged_verify_causal(device):
     run_case(device, 78, 3, 8, 2, 4, 900, 128, 2, 1, lengths=[4, 900, 517], causal=True)
 

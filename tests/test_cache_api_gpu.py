@@ -211,3 +211,42 @@ def test_generate_loop_replay_matches_oracle(device):
         from tests.test_attention_gpu import assert_close
 
         assert_close(out, want, "bf16", f"layer {i}")
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_dense_rotation_cache_end_to_end(device, d):
+    """rotation="dense": matrix-core append, then decode and verify through the cache API."""
+    from tests.test_append_dense_gpu import BAND
+    from tests.test_attention_gpu import assert_close
+
+    B, Hq, Hkv = 2, 8, 4
+    g = torch.Generator(device="cpu").manual_seed(d)
+    k = torch.randn(B, Hkv, 600, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, 600, d, generator=g).to(torch.bfloat16)
+    cache = TurboQuantKVCache(bits=3.5, rotation="dense")     # K 3-bit, V 4-bit
+    cache.update_and_fetch(k[:, :, :597].to(device), v[:, :, :597].to(device))
+    ks, vs = cache.update_and_fetch(k[:, :, 597:].to(device), v[:, :, 597:].to(device))
+    kr, vr = O.rotation_matrix(d, 0), O.rotation_matrix(d, 1)
+    kcb, vcb = O.beta_codebook(d, 3), O.beta_codebook(d, 4)
+    kp, kn, ky = O.quantize_dense(k.float().numpy(), 3, kr, kcb)
+    vp, vn, vy = O.quantize_dense(v.float().numpy(), 4, vr, vcb)
+    st = cache.state
+    assert np.array_equal(st[0].norms.cpu().numpy(), kn)
+    assert np.array_equal(st[1].norms.cpu().numpy(), vn)
+    for got, want, y, bits, cb in ((st[0].indices, kp, ky, 3, kcb), (st[1].indices, vp, vy, 4, vcb)):
+        gi = O.unpack_lowbit(got.cpu().numpy().astype(np.uint32), bits, d).astype(np.int64)
+        wi = O.unpack_lowbit(want, bits, d).astype(np.int64)
+        bad = gi != wi
+        if bad.any():
+            dist = np.abs(y[bad][:, None].astype(np.float64) - O.midpoints(cb)[None, :]).min(axis=1)
+            assert dist.max() <= BAND
+    # attention over the cache's own packed state (decode, then a causal verify of 3 rows)
+    gp = [s_.indices.cpu().numpy().astype(np.uint32) for s_ in st]
+    for L in (1, 3):
+        q = torch.randn(B, Hq, L, d, generator=g).to(torch.bfloat16)
+        mask = "causal" if L > 1 else None
+        out = scaled_dot_product_attention(q.to(device), ks, vs, cache, 1 / math.sqrt(d), mask)
+        want = O.attention(q.float().numpy(), gp[0], kn, gp[1], vn, k_bits=3, v_bits=4,
+                           k_codebook=kcb, v_codebook=vcb, rot_kind="dense", k_rot=kr, v_rot=vr,
+                           scale=1 / math.sqrt(d), q_dtype="bf16", causal=L > 1)
+        assert_close(out, want, "bf16", f"dense cache d{d} L{L}")
