@@ -678,6 +678,12 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
     }
     wave_sync();
     const u32x4_t A = *reinterpret_cast<const u32x4_t*>(w_mine + n * SUB + 8 * g);
+    // value products run hi/lo in the k dimension: k-slots
+    // [a hi, b hi, a lo, b lo, c hi, d hi, c lo, d lo] against weights
+    // [w_a, w_b, w_a, w_b, w_c, w_d, w_c, w_d], so one 8-byte table read (the
+    // hi pair and the lo pair of two tokens) fills half a B operand in place
+    const u32x4_t A0 = {A[0], A[0], A[1], A[1]};
+    const u32x4_t A1 = {A[2], A[2], A[3], A[3]};
     // ---- values: interleave the two tokens of each pair, one key per coordinate
     constexpr uint32_t MEVEN = [] {
       uint32_t m = 0;
@@ -707,16 +713,14 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
     for (int c = 0; c < CPL; ++c) {
       const int k = c / SEGC;
       const int cc = c % SEGC;
-      u32x4_t bh, bl;
+      uint2 v[4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
         const uint32_t z[1] = {(cc & 1) ? zh[e2][k] : zl[e2][k]};
-        const uint2 v = lds_at<uint2>(lds, key_addr<2 * VB, S::LOGSV>(z, (cc >> 1) * 2 * VB, lutv_lane, vmask));
-        bh[e2] = v.x;
-        bl[e2] = v.y;
+        v[e2] = lds_at<uint2>(lds, key_addr<2 * VB, S::LOGSV>(z, (cc >> 1) * 2 * VB, lutv_lane, vmask));
       }
-      O[c] = mfma_f16(A, bl, O[c]);
-      O[c] = mfma_f16(A, bh, O[c]);
+      O[c] = mfma_f16(A0, u32x4_t{v[0].x, v[0].y, v[1].x, v[1].y}, O[c]);
+      O[c] = mfma_f16(A1, u32x4_t{v[2].x, v[2].y, v[3].x, v[3].y}, O[c]);
     }
   };
 
