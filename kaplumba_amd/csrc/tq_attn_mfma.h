@@ -146,19 +146,26 @@ struct MfmaShape {
   static constexpr int LOGSV = REPV == 64 ? 9 : 7;  // log2(REPV * 8): (hi pair, lo pair) entries
   static constexpr int LUTK_BYTES = KKEYS * REPK * 8;
   static constexpr int LUTV_BYTES = VKEYS * REPV * 8;
-  static constexpr int LUTK_OFF = 0;      // keys: 32 KiB block
-  static constexpr int LUTV_OFF = 32768;  // values: 32 KiB block
+  static constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
+  static constexpr int BK = pow2ceil(LUTK_BYTES);  // table blocks: power-of-two sizes,
+  static constexpr int BV = pow2ceil(LUTV_BYTES);  // each aligned to its size
+  static constexpr int LUTK_OFF = BK >= BV ? 0 : BV;
+  static constexpr int LUTV_OFF = BK >= BV ? BK : 0;
   static constexpr int QSTRIDE = D + 4;   // padded rows: the 16 rows read apart land on distinct banks
-  static constexpr int Q_OFF = 65536;     // [NQ][QSTRIDE] f32 rotated queries
+  static constexpr int Q_OFF = BK + BV;   // [NQ][QSTRIDE] f32 rotated queries
   static constexpr int QS_OFF = Q_OFF + NQ * QSTRIDE * 4;  // [NQ] f32 max |q_rot| per row
-  static constexpr int W_OFF = QS_OFF + 64;            // [NW][16][32] f16 weights
-  static constexpr int CO_OFF = W_OFF + NW * 16 * SUB * 2;  // [NW][NQ][D] f32 wave outputs
+  static constexpr int W_OFF = QS_OFF + 64;                // [NW][16][32] f16 weights
+  static constexpr int LOOP_BYTES = W_OFF + NW * 16 * SUB * 2;
+  // after the token loop the buffers above are dead: the epilogue's buffers
+  // start again at 0 (a barrier separates the two phases)
+  static constexpr int CO_OFF = 0;                          // [NW][NQ][D] f32 wave outputs
   static constexpr int CM_OFF = CO_OFF + NW * NQ * D * 4;
   static constexpr int CL_OFF = CM_OFF + NW * NQ * 4;
   static constexpr int O_OFF = CL_OFF + NW * NQ * 4;  // [NQ][D] combined rows
   static constexpr int ML_OFF = O_OFF + NQ * D * 4;   // [NQ][2]
   static constexpr int AUX_OFF = ML_OFF + (NQ * 8 + 15) / 16 * 16;  // [NQ + D] f32 finalize scratch
-  static constexpr int BYTES = AUX_OFF + (NQ + D) * 4;
+  static constexpr int POST_BYTES = AUX_OFF + (NQ + D) * 4;
+  static constexpr int BYTES = LOOP_BYTES > POST_BYTES ? LOOP_BYTES : POST_BYTES;
   static constexpr int RPW = (NQ + NW - 1) / NW;  // query rows rotated per wave
   static constexpr int QPL = D / kWave;           // query elements per lane and row
   static_assert(D % 64 == 0, "head dim");
@@ -742,6 +749,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   }
 
   // --------------------------------------------------- combine the waves ----
+  lds_barrier();  // every wave is done with the tables, queries and weights
   const float oscale = ldexpf(1.f, E) / cbs_v;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
