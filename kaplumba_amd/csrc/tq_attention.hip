@@ -100,16 +100,11 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
   SplitPlan sp{};
   const int R = Hq / Hkv;
   const int rows = R * L;
-  if (packed) {
-    // matrix-core kernel: 16-row tiles; 4-row groups when the GQA group is
-    // small (less LDS and fewer partial rows), and for d = 256 (registers)
-    sp.nq = (rows <= 4 || D >= 256) ? 4 : 16;
-  } else {
-    // plain kernel: d = 256 keeps two rows so q and o fit in registers
-    const int nq_max = D >= 256 ? 2 : 4;
-    sp.nq = rows >= 4 ? 4 : (rows >= 2 ? 2 : 1);
-    if (sp.nq > nq_max) sp.nq = nq_max;
-  }
+  // matrix-core kernels (packed and plain): 16-row tiles; 4-row groups when
+  // the GQA group is small (less LDS and fewer partial rows), and for d = 256
+  // (registers).  A row group reads its kv head's cache once.
+  (void)packed;
+  sp.nq = (rows <= 4 || D >= 256) ? 4 : 16;
   sp.n_rg = (rows + sp.nq - 1) / sp.nq;
   const int64_t base = static_cast<int64_t>(B) * Hkv * sp.n_rg;
   // workgroups in flight per CU the split count aims for (KAPLUMBA_TQ_WG_PER_CU)
@@ -141,12 +136,6 @@ int64_t workspace_bytes(const SplitPlan& sp, int B, int Hq, int Hkv, int L, int 
          align256(grows * sp.n_splits * 2 * 4);
 }
 
-size_t attn_lds_bytes(const SplitPlan& sp, int D) {
-  const size_t w = static_cast<size_t>(sp.chunk) * sp.nq;               // scores / weights
-  const size_t o = static_cast<size_t>(kAttnWaves) * sp.nq * D;         // wave fold
-  const size_t m = static_cast<size_t>(merge_scratch_floats(sp.nq, D));  // merge scratch
-  return std::max(w, std::max(o, m)) * sizeof(float);
-}
 
 }  // namespace tq
 
@@ -200,6 +189,9 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   } else if (kv_kind == TQ_KV_PLAIN) {
     if (kv_dtype != TQ_DTYPE_F16 && kv_dtype != TQ_DTYPE_BF16)
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: plain kv_dtype %d", kv_dtype);
+    if (capacity * static_cast<int64_t>(dim) * 2 > UINT32_MAX)
+      return fail(TQ_ERR_UNSUPPORTED, "attention: a plain row of %lld tokens exceeds 4 GiB",
+                  (long long)capacity);
   } else {
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: kv_kind %d", kv_kind);
   }
@@ -235,7 +227,7 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   p.norm_dtype = norm_dtype;
   p.kcb = k_codebook;
   p.vcb = v_codebook;
-  p.rot_kind = rot_kind;
+  p.rot_kind = kv_kind == TQ_KV_PLAIN ? TQ_ROT_HADAMARD : rot_kind;  // plain: no rotation is read
   p.krot = k_rot;
   p.vrot = v_rot;
   p.seq_lens = seq_lens;
@@ -281,8 +273,8 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
     case 128: rc = launch_partial_d128(p, kv_kind, kv_dtype, k_bits, v_bits, st); break;
     default: rc = launch_partial_d256(p, kv_kind, kv_dtype, k_bits, v_bits, st); break;
   }
-  if (rc || kv_kind != TQ_KV_PACKED || sp.n_splits == 1) return rc;
-  // packed caches: the splits' partials are merged by a second kernel
+  if (rc || sp.n_splits == 1) return rc;
+  // the splits' partials are merged by a second kernel
   // one workgroup per query row; for the dense rotation one per 64 output
   // columns of a row group (R_V^-1 is read once per row group)
   const unsigned mx = rot_kind == TQ_ROT_DENSE ? static_cast<unsigned>(dim / 64) : static_cast<unsigned>(sp.nq);

@@ -1,14 +1,7 @@
-// Split-K publication and merge shared by the attention kernels.
-//
-// Each workgroup ends with its split's (max m, sum l, o[D]) per query row in
-// LDS (o unnormalised, in rotated space).  It stores them to the workspace
-// with agent-scope (sc1, write-through) stores, waits for the stores to
-// complete, and bumps the group's counter.  The workgroup that brings the
-// counter to the number of live splits merges: it reads every split with
-// agent-scope loads (so no stale L2 line from another XCD is used), combines
-// them by log-sum-exp, divides by max(l, 1e-6), applies R_V^-1 and stores the
-// rows in the query dtype.  No cache-wide write-back or invalidate is needed
-// because every shared value goes through sc1 accesses.
+// Helpers shared by the attention kernels: query / output dtype access, the
+// query rows of a row group (RowSet), and the finish of a problem that fits
+// one split (normalise by 1/max(l, 1e-6), apply R_V^-1, store in the query
+// dtype).  Problems with several splits are merged by attn_merge_kernel.
 #pragma once
 
 #include "tq_attention.h"
@@ -35,17 +28,10 @@ __device__ __forceinline__ void store_out(void* o, int dt, int64_t i, float v) {
     static_cast<uint16_t*>(o)[i] = f32_to_bf16_bits(v);
 }
 
-__device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // In-place unnormalised Walsh-Hadamard transform of NQ rows of length D in
 // LDS (stride D), all NT threads of the block participating.
-template <int D, int NQ, int NT = kAttnThreads>
+template <int D, int NQ, int NT>
 __device__ __forceinline__ void lds_fwht(float* y) {
 #pragma unroll 1
   for (int hs = 1; hs < D; hs <<= 1) {
@@ -88,7 +74,7 @@ struct RowSet {
 
 // Normalise s_o rows by 1/max(l, eps), apply R_V^-1 and store.  s_o: [NQ][D];
 // s_vsign: D floats of LDS scratch.
-template <int D, int NQ, int NT = kAttnThreads>
+template <int D, int NQ, int NT>
 __device__ void finalize_rows(const AttnParams& p, const RowSet& rs, float* s_o,
                               const float* s_l, float* s_vsign, bool plain, bool dense) {
   if (!plain && !dense)
@@ -114,135 +100,6 @@ __device__ void finalize_rows(const AttnParams& p, const RowSet& rs, float* s_o,
     }
     store_out(p.out, p.q_dtype, rs.qoff(j) * D + d, r);
   }
-}
-
-// Publish this workgroup's split and, in the last workgroup of the group,
-// merge all splits and write the output.
-//   s_o  [NQ][D] LDS: o of this split (rotated space, true scale)
-//   s_ml [NQ][2] LDS: (m, l) of this split
-//   scratch: LDS of at least merge_scratch_floats(NQ, D, NT) floats
-//   s_aux: LDS of at least NQ + D floats; s_flag: one int of LDS
-// Workspace layout per group g = (b, kv head, row group):
-//   po [g][split][NQ][D], pml [g][split][NQ][2]   (contiguous per split)
-template <int D, int NQ, int NT = kAttnThreads>
-__device__ void publish_and_merge(const AttnParams& p, const RowSet& rs, float* s_o,
-                                  float* s_ml, float* scratch, float* s_aux, int* s_flag,
-                                  int64_t grp, int split, int nvalid, bool plain, bool dense) {
-  const int tid = threadIdx.x;
-  float* s_tot = s_aux;        // [NQ]
-  float* s_vsign = s_aux + NQ;  // [D]
-
-  if (nvalid == 1) {  // the only split: finish from LDS
-    if (tid < NQ) s_tot[tid] = s_ml[2 * tid + 1];
-    __syncthreads();
-    finalize_rows<D, NQ, NT>(p, rs, s_o, s_tot, s_vsign, plain, dense);
-    return;
-  }
-
-  float* po_g = p.po + grp * static_cast<int64_t>(p.n_splits) * NQ * D;
-  float* pml_g = p.pml + grp * static_cast<int64_t>(p.n_splits) * NQ * 2;
-  for (int idx = tid; idx < NQ * D; idx += NT)
-    st_agent(po_g + static_cast<int64_t>(split) * NQ * D + idx, s_o[idx]);
-  if (tid < 2 * NQ) st_agent(pml_g + static_cast<int64_t>(split) * NQ * 2 + tid, s_ml[tid]);
-  __builtin_amdgcn_s_waitcnt(0);  // every sc1 store of this thread has completed
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(p.counters + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = (prev + 1 == static_cast<uint32_t>(nvalid)) ? 1 : 0;
-    if (last) __hip_atomic_store(p.counters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = last;
-  }
-  __syncthreads();
-  if (!*s_flag) return;
-
-  // ---- merge (last workgroup only).  Thread t owns float4 column c of row j
-  // (several, when NQ * D / 4 > NT) for the splits sg, sg + SG, ...; it loads
-  // a batch of them with independent loads, folds them with an online
-  // log-sum-exp, and the SG thread groups of a (row, column) fold through LDS
-  // at the end.
-  constexpr int C4 = D / 4;
-  constexpr int COLS = C4 * NQ;                 // (row, float4 column) pairs
-  constexpr int SG = COLS >= NT ? 1 : NT / COLS;  // split groups
-  constexpr int BATCH = 16;                     // splits per thread per round trip
-  static_assert(COLS >= NT ? COLS % NT == 0 : NT % COLS == 0, "merge mapping");
-  float* s_po = scratch;  // [SG][NQ][D] o, then [SG][NQ] m and l
-  float* s_pm = scratch + SG * NQ * D;
-  float* s_pl = s_pm + SG * NQ;
-  for (int col = tid % (SG == 1 ? NT : COLS); col < COLS; col += (SG == 1 ? NT : COLS)) {
-    const int c = col % C4;
-    const int j = col / C4;
-    const int sg = SG == 1 ? 0 : tid / COLS;
-    float M = -INFINITY, Ls = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int sp0 = sg; sp0 < nvalid; sp0 += SG * BATCH) {
-      float mm[BATCH], ll[BATCH];
-      float4 oo[BATCH];
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int sp = sp0 + u * SG;
-        if (sp < nvalid) {
-          const float* e = pml_g + (static_cast<int64_t>(sp) * NQ + j) * 2;
-          const float* o4 = po_g + (static_cast<int64_t>(sp) * NQ + j) * D + 4 * c;
-          mm[u] = ld_agent(e);
-          ll[u] = ld_agent(e + 1);
-          oo[u] = make_float4(ld_agent(o4), ld_agent(o4 + 1), ld_agent(o4 + 2), ld_agent(o4 + 3));
-        } else {
-          mm[u] = -INFINITY;
-          ll[u] = 0.f;
-          oo[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-      float bm = M;
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) bm = fmaxf(bm, mm[u]);
-      const float r = (M == -INFINITY) ? 0.f : __expf(M - bm);
-      Ls *= r;
-      acc.x *= r;
-      acc.y *= r;
-      acc.z *= r;
-      acc.w *= r;
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const float sc = (mm[u] == -INFINITY) ? 0.f : __expf(mm[u] - bm);
-        Ls = fmaf(sc, ll[u], Ls);
-        acc.x = fmaf(sc, oo[u].x, acc.x);
-        acc.y = fmaf(sc, oo[u].y, acc.y);
-        acc.z = fmaf(sc, oo[u].z, acc.z);
-        acc.w = fmaf(sc, oo[u].w, acc.w);
-      }
-      M = bm;
-    }
-    reinterpret_cast<float4*>(s_po + (sg * NQ + j) * D)[c] = acc;
-    if (c == 0) {
-      s_pm[sg * NQ + j] = M;
-      s_pl[sg * NQ + j] = Ls;
-    }
-  }
-  __syncthreads();
-  for (int idx = tid; idx < NQ * D; idx += NT) {
-    const int jj = idx / D;
-    float Mt = -INFINITY;
-#pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) Mt = fmaxf(Mt, s_pm[g2 * NQ + jj]);
-    float a = 0.f, lt = 0.f;
-#pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) {
-      const float m2 = s_pm[g2 * NQ + jj];
-      const float sc = (m2 == -INFINITY) ? 0.f : __expf(m2 - Mt);
-      a = fmaf(sc, s_po[(g2 * NQ) * D + idx], a);
-      lt = fmaf(sc, s_pl[g2 * NQ + jj], lt);
-    }
-    s_o[idx] = a;
-    if (idx % D == 0) s_tot[jj] = lt;
-  }
-  __syncthreads();
-  finalize_rows<D, NQ, NT>(p, rs, s_o, s_tot, s_vsign, plain, dense);
-}
-
-// Dynamic LDS the merge needs (floats).
-__host__ __device__ constexpr int merge_scratch_floats(int nq, int d, int nt = kAttnThreads) {
-  return ((d / 4) * nq >= nt ? 1 : nt / ((d / 4) * nq)) * nq * (d + 2) + 4;
 }
 
 }  // namespace tq

@@ -29,11 +29,11 @@
 //     Output: lane (g, n), register i = row 4g + i, coordinate (D/16)*n + c.
 // Codebook lookups go through small pair tables in LDS (two coordinates or
 // two tokens per entry), replicated so the 16 lanes of a row hit distinct
-// banks.  Weights are p * ||v|| scaled by a per-wave power of two into
-// [0, 1] and stored in f16; the value table uses a codebook scale searched
-// for the smallest worst-case relative f16 error (identically in every
-// workgroup), so the f16 rounding leaves no common bias in the rotated
-// coordinates for the inverse Hadamard transform to pile into one output.
+// banks.  Table entries hold hi + lo f16 parts of the scaled codebook values
+// (~22 significant bits): a single f16 would leave a per-entry rounding error
+// that every token with that index repeats, i.e. a bias that does not average
+// out over the context.  Weights are p * ||v|| scaled by a per-wave power of
+// two into [0, 1] and stored in f16 (their rounding is independent per token).
 #pragma once
 
 #include "tq_attn_merge.h"

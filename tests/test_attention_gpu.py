@@ -215,3 +215,34 @@ def test_config1_full_size(device):
                        rot_kind="hadamard", k_rot=O.rht_signs(128, 0), v_rot=O.rht_signs(128, 1),
                        scale=1 / math.sqrt(128), q_dtype="bf16")
     assert_close(out, want, "bf16", "config1")
+
+
+@pytest.mark.parametrize("kvdt", ["f16", "bf16"])
+@pytest.mark.parametrize("d,Hq,Hkv,L,T,lengths", [
+    (128, 32, 8, 4, 5000, None),        # cfg4 shape at reduced length: 16-row groups, causal
+    (128, 8, 8, 1, 3000, None),         # MHA decode, 4-row groups, many splits
+    (64, 16, 2, 1, 2600, [2600, 17]),   # ragged, 16-row groups (GQA 8 x 2 rows)
+    (256, 16, 8, 3, 2300, [900, 2300]), # d=256 verify, ragged
+    (128, 4, 1, 1, 200, None),          # one split: finished inside the partial kernel
+])
+def test_plain_layers(device, kvdt, d, Hq, Hkv, L, T, lengths):
+    """fp16 / bf16 layers (the mixed-precision split) through the matrix-core plain kernel."""
+    rng = np.random.default_rng(d + L + T)
+    B = 2 if lengths is not None else 1
+    tdt = TORCH_QDT[kvdt]
+    s = np.exp(rng.normal(0, 0.5, size=(1, Hkv, 1, d)))
+    k = torch.from_numpy((rng.standard_normal((B, Hkv, T, d)) * s).astype(np.float32)).to(tdt)
+    v = torch.from_numpy((rng.standard_normal((B, Hkv, T, d)) * s).astype(np.float32)).to(tdt)
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, d)).astype(np.float32), "bf16")
+    causal = L > 1
+    want = O.attention_plain(q, k.float().numpy(), v.float().numpy(), scale=1 / math.sqrt(d),
+                             q_dtype="bf16", causal=causal, lengths=lengths)
+    cap = T + 9
+    kb = torch.zeros((B, Hkv, cap, d), dtype=tdt, device=device)
+    vb = torch.zeros_like(kb)
+    kb[:, :, :T] = k.to(device)
+    vb[:, :, :T] = v.to(device)
+    sl = torch.tensor(lengths, dtype=torch.int32, device=device) if lengths is not None else None
+    out = ops.attention_plain(q_tensor(q, "bf16", device), kb[:, :, :T], vb[:, :, :T],
+                              1 / math.sqrt(d), causal, seq_lens=sl)
+    assert_close(out, want, "bf16", f"plain {kvdt} d{d} Hq{Hq} Hkv{Hkv} L{L} T{T}")
