@@ -14,6 +14,8 @@
 //   * y = v * f32(1/sqrt(D)); idx = #{m : y > mid[m]} (strict compare);
 //   * a lane's 32 indices fill exactly `bits` consecutive words of the
 //     LSB-first stream, so packing is thread-local (no shared-word races).
+#include <type_traits>
+
 #include "tq_append.h"
 
 namespace tq {
@@ -59,11 +61,24 @@ __global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
   constexpr int VPB = 256 / NL;       // vectors per block
   constexpr int NMID = (1 << BITS) - 1;
   constexpr int PW = D * BITS / 32;
+  constexpr bool LUT = NMID > 3;  // bucket table beyond three midpoints
   __shared__ float s_sign[D];
   __shared__ float s_mid[NMID];
+  __shared__ uint2 s_qb[LUT ? kQbN : 1];
+  __shared__ int s_qb_bad;
   for (int i = threadIdx.x; i < D; i += blockDim.x) s_sign[i] = a.rot[i];
   if (threadIdx.x < NMID) s_mid[threadIdx.x] = a.mid[threadIdx.x];
+  if (threadIdx.x == 0) s_qb_bad = 0;
   __syncthreads();
+  if constexpr (LUT) {
+    for (int t = threadIdx.x; t < kQbN; t += blockDim.x) {
+      uint2 ent;
+      if (!qb_entry(t, s_mid, NMID, ent)) s_qb_bad = 1;
+      s_qb[t] = ent;
+    }
+    __syncthreads();
+  }
+  const bool use_lut = LUT && s_qb_bad == 0;
 
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
   const int64_t vec = static_cast<int64_t>(blockIdx.x) * VPB + threadIdx.x / NL;
@@ -91,8 +106,10 @@ __global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
     for (int i = 0; i < w; ++i) s[i] = __fadd_rn(s[i], s[i + w]);
   }
   float ss = s[0];
-#pragma unroll
-  for (int off = 1; off < NL; off <<= 1) ss = __fadd_rn(ss, __shfl_xor(ss, off, kWave));
+  if constexpr (NL >= 2) ss = __fadd_rn(ss, xor_lane<1>(ss));
+  if constexpr (NL >= 4) ss = __fadd_rn(ss, xor_lane<2>(ss));
+  if constexpr (NL >= 8) ss = __fadd_rn(ss, xor_lane<4>(ss));
+  if constexpr (NL >= 16) ss = __fadd_rn(ss, xor_lane<8>(ss));
   const float n = sqrt_rn(ss);
   const float den = fmaxf(n, kNormEps);
 
@@ -113,32 +130,48 @@ __global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
       }
     }
   }
-  // ---- cross-lane stages (distance 32, 64, ...): lane bit j <-> element bit 5+j
+  // ---- cross-lane stages (distance 32, 64, ...): lane bit j <-> element bit 5+j;
+  // the upper lane of a pair forms p - v, the lower v + p, both as one
+  // rounding of v * (+-1) + p (the product is exact)
+  auto cross = [&](auto off_tag) {
+    constexpr int OFF = decltype(off_tag)::value;
+    const float sg = (g & OFF) != 0 ? -1.f : 1.f;
 #pragma unroll
-  for (int off = 1; off < NL; off <<= 1) {
-    const bool upper = (g & off) != 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float p = __shfl_xor(v[i], off, kWave);
-      v[i] = upper ? __fsub_rn(p, v[i]) : __fadd_rn(v[i], p);
-    }
-  }
+    for (int i = 0; i < 32; ++i) v[i] = __builtin_fmaf(v[i], sg, xor_lane<OFF>(v[i]));
+  };
+  if constexpr (NL >= 2) cross(std::integral_constant<int, 1>{});
+  if constexpr (NL >= 4) cross(std::integral_constant<int, 2>{});
+  if constexpr (NL >= 8) cross(std::integral_constant<int, 4>{});
+  if constexpr (NL >= 16) cross(std::integral_constant<int, 8>{});
 
   // ---- scale, quantize against midpoints, pack thread-locally
   uint32_t words[BITS];
+  auto pack_all = [&](auto idx_of) {
 #pragma unroll
-  for (int w = 0; w < BITS; ++w) words[w] = 0u;
+    for (int w = 0; w < BITS; ++w) words[w] = 0u;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const float y = __fmul_rn(v[i], a.scale);
-    uint32_t idx = 0;
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t idx = idx_of(__fmul_rn(v[i], a.scale));
+      const int pos = i * BITS;
+      const int wi = pos >> 5;
+      const int sh = pos & 31;
+      words[wi] |= idx << sh;
+      if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
+    }
+  };
+  // a NaN / infinite norm makes every y NaN, and NaN compares below every midpoint
+  if (use_lut && n < INFINITY) {
+    pack_all([&](float y) -> uint32_t {
+      const uint2 ent = s_qb[qb_index(y)];
+      return ent.x + ((y > __uint_as_float(ent.y)) ? 1u : 0u);
+    });
+  } else {
+    pack_all([&](float y) -> uint32_t {
+      uint32_t idx = 0;
 #pragma unroll
-    for (int m = 0; m < NMID; ++m) idx += (y > s_mid[m]) ? 1u : 0u;
-    const int pos = i * BITS;
-    const int wi = pos >> 5;
-    const int sh = pos & 31;
-    words[wi] |= idx << sh;
-    if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
+      for (int m = 0; m < NMID; ++m) idx += (y > s_mid[m]) ? 1u : 0u;
+      return idx;
+    });
   }
 
   const int64_t row = (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l;

@@ -118,6 +118,67 @@ __device__ __forceinline__ float sqrt_rn(float x) {
   return small ? s * 0x1p-16f : s;
 }
 
+// ------------------------------------------------- quantization buckets ----
+// idx(y) = #{m : y > mid_m} for sorted midpoints through one table lookup.
+// y is bucketed by bits 30..20 of its magnitude (the 8 exponent bits and the
+// top 3 mantissa bits: a monotone image of |y|), clamped so that bucket 0
+// holds |y| < 2^-24 and the last bucket |y| >= 2 (and inf / NaN); negative y
+// use a mirrored copy, so the table index is monotone in y.  Entry t holds
+// (number of midpoints below the bucket, the midpoint inside it or +inf);
+// the lookup is exact whenever no bucket holds two midpoints (the buckets are
+// 1/8 of a binade wide, Lloyd-Max midpoints are much farther apart), which
+// qb_entry reports so that a kernel can fall back to plain comparisons.
+constexpr uint32_t kQbLo = 823;                 // (bits >> 20) of 2^-24 is 824
+constexpr uint32_t kQbHi = 1024;                // (bits >> 20) of 2.0
+constexpr int kQbHalf = kQbHi - kQbLo + 1;      // 202 buckets per sign
+constexpr int kQbN = 2 * kQbHalf;               // 404 table entries
+
+__device__ __forceinline__ uint32_t qb_index(float y) {
+  const uint32_t u = __float_as_uint(y);
+  const uint32_t e = min(max((u >> 20) & 0x7ffu, kQbLo), kQbHi) - kQbLo;  // 0 .. 201
+  const uint32_t sm = static_cast<uint32_t>(static_cast<int32_t>(u) >> 31);
+  return kQbHalf + (e ^ sm);  // y >= +0: 202 + e; y <= -0: 202 + ~e = 201 - e
+}
+
+// Table entry t for the nmid sorted midpoints; returns false when two
+// midpoints share the bucket.
+__device__ __forceinline__ bool qb_entry(int t, const float* mid, int nmid, uint2& ent) {
+  const bool neg = t < kQbHalf;
+  const int e = neg ? (kQbHalf - 1 - t) : (t - kQbHalf);
+  const float alo = e == 0 ? 0.f : __uint_as_float((static_cast<uint32_t>(e) + kQbLo) << 20);
+  const float ahi = e == static_cast<int>(kQbHi - kQbLo)
+                        ? INFINITY
+                        : __uint_as_float((static_cast<uint32_t>(e) + kQbLo + 1) << 20);
+  uint32_t base = 0;
+  int inside = 0;
+  float thr = INFINITY;
+  for (int m = 0; m < nmid; ++m) {
+    const float md = mid[m];
+    if (!neg) {  // y in [alo, ahi)
+      if (md < alo) ++base;
+      else if (md < ahi) { ++inside; thr = md; }
+    } else {     // y in (-ahi, -alo]
+      if (md <= -ahi) ++base;
+      else if (md <= -alo) { ++inside; thr = md; }
+    }
+  }
+  ent = make_uint2(base, __float_as_uint(thr));
+  return inside <= 1;
+}
+
+// Lane value of the partner lane ^ OFF (OFF < 32): DPP inside a quad, a
+// swizzle beyond.
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (OFF == 1)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, true));  // quad_perm [1,0,3,2]
+  else if constexpr (OFF == 2)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, true));  // quad_perm [2,3,0,1]
+  else
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1f | (OFF << 10)));  // bit mode: lane ^ OFF
+}
+
 // ----------------------------------------------------------- bit fields ----
 // Value of bits [pos, pos+nb) of a little-endian word array held in registers.
 // pos and nb are compile-time after unrolling, so this folds to v_bfe_u32 or
