@@ -63,6 +63,11 @@ struct SplitPlan {
 };
 
 SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool packed);
+
+// Packed caches whose row group is at most 4 query rows (GQA decode with
+// R <= 4, or verify with R * L <= 4) at head dim 64 / 128 run the small
+// row-group kernel (tq_attn_small.h).
+bool small_rows_path(int kv_kind, int D, int rows);
 int64_t workspace_bytes(const SplitPlan& p, int B, int Hq, int Hkv, int L, int D);
 
 // Kernel launchers instantiated per head dim in tq_attn_d*.hip.

@@ -96,6 +96,15 @@ void launch_qprep(const AttnParams& p, int q_dtype, int64_t rows, hipStream_t st
 }
 
 // ------------------------------------------------------------- planning ---
+bool small_rows_path(int kv_kind, int D, int rows) {
+  // KAPLUMBA_TQ_SMALL_ROWS=0 selects the general kernel + merge kernel instead
+  static const bool enabled = [] {
+    const char* e = getenv("KAPLUMBA_TQ_SMALL_ROWS");
+    return !(e && e[0] == '0');
+  }();
+  return enabled && kv_kind == TQ_KV_PACKED && D <= 128 && rows <= 4;
+}
+
 SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool packed) {
   SplitPlan sp{};
   const int R = Hq / Hkv;

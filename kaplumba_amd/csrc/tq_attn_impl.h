@@ -7,11 +7,26 @@
 
 #include "tq_attn_mfma.h"
 #include "tq_attn_plain.h"
+#include "tq_attn_small.h"
 
 namespace tq {
 
 template <int D, int KB>
+int launch_small_vb(const AttnParams& p, int vb, hipStream_t st) {
+  switch (vb) {
+    case 1: return launch_small<D, KB, 1>(p, st);
+    case 2: return launch_small<D, KB, 2>(p, st);
+    case 3: return launch_small<D, KB, 3>(p, st);
+    case 4: return launch_small<D, KB, 4>(p, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
+}
+
+template <int D, int KB>
 int launch_partial_vb(const AttnParams& p, int vb, hipStream_t st) {
+  if constexpr (D <= 128) {
+    if (small_rows_path(TQ_KV_PACKED, D, p.R * p.L)) return launch_small_vb<D, KB>(p, vb, st);
+  }
   switch (vb) {
     case 1: return launch_mfma_nq<D, KB, 1>(p, st);
     case 2: return launch_mfma_nq<D, KB, 2>(p, st);

@@ -1,0 +1,664 @@
+// TurboQuant decode / verify attention for small row groups (at most 4 query
+// rows per kv head: GQA decode with R <= 4, or verify with R * L <= 4) and
+// head dims 64 / 128, straight from packed indices.
+//
+// Workgroup: 8 wave64s own tokens [t_begin, t_end) of one (sequence, kv head)
+// and all (<= 4) query rows of its GQA group.  Tokens are cut into 32-token
+// sub-chunks; sub-chunk i belongs to wave i % 8, and each wave keeps the
+// global loads of its next P sub-chunks in flight.
+//
+// Lane roles (l = lane, n = l % 16, g = l / 16):
+//   scores  S^T[tok][col] = sum_d k[tok][d] * q_col[d]    (16 x 16 tile, 32 tokens)
+//     A = keys: lane (m, g) holds token 16 (g >> 1) + m, coordinate half
+//         g & 1 (D/2 coordinates: a contiguous bit span of its packed row),
+//         eight coordinates per MFMA, hi parts in one MFMA and lo parts in
+//         the next (f16 hi + lo carry ~22 significant bits),
+//     B = queries: column n = 8p + 4j + r is piece p (hi / lo f16 split) of
+//         query row r for token subset j; the k slots of lane groups that
+//         hold the other subset's tokens are zero.  So every output element
+//         is useful: lane (g', n) register i holds piece p of the score of
+//         token 16j + 4g' + i against row r, and one DPP row rotation by 8
+//         adds the two pieces (f32 accuracy: (q_hi + q_lo)(k_hi + k_lo)).
+//   softmax per lane: 4 tokens of one row (both pieces' lanes hold copies).
+//   values  O[row][d] = sum_tok w[row][tok] * v[tok][d]      (16 x 16 tiles)
+//     A = weights: lane (row r, g) holds tokens 4g .. 4g+3 and 16+4g .. 16+4g+3
+//         as f16: its own four scores' weights plus those of lane n + 4
+//         (token subset 1), fetched with one DPP rotation; no LDS transpose,
+//     B = values: lane (coordinate n of tile c, g) holds the same 8 tokens'
+//         codebook values as (hi pair, lo pair) of two tokens per 8-byte
+//         table read (the table is keyed by the two tokens' fields), against
+//         weights (w_a, w_b, w_a, w_b): four tokens per MFMA and lane group.
+//     Output: lane (g = 0, n), register i = row i, coordinate (D/16) n + c.
+// Codebook lookups go through pair tables in LDS (keys: hi and lo f16 halves
+// in two tables sharing one key address; values: one 8-byte entry),
+// replicated per lane so that the lanes of one read hit distinct banks.
+//
+// Softmax: base 2 with log2(e) and the hi/lo scales folded into one factor;
+// the reference maximum moves lazily (only when a score exceeds it by 2^7),
+// and weights p * ||v|| * 2^-E carry a per-wave value-norm exponent E that
+// keeps them inside f16 range, so the common sub-chunk takes no reductions.
+//
+// Splits: a problem with one split is finished here; otherwise every
+// workgroup writes its (o, m, l) partial (o already through R_V^-1 for the
+// Hadamard rotation, m in natural-log units) in the layout attn_merge_kernel
+// reads, and that kernel merges them on the same stream.  (A last-arriver
+// merge inside this kernel costs more: its store -> wait -> count -> load
+// chain is four serial memory round trips, against one launch gap.)
+// Semantics: quantized_attention, turboquant_cache.py:5110-5203.
+#pragma once
+
+#include "tq_attn_mfma.h"
+
+namespace tq {
+
+template <int D, int KB, int VB>
+struct SmallShape {
+  static constexpr int NW = 8;
+  static constexpr int NT = NW * kWave;
+  static constexpr int SUB = 32;  // tokens per sub-chunk
+#ifndef TQ_SMALL_PREFETCH
+#define TQ_SMALL_PREFETCH 2
+#endif
+  static constexpr int P = TQ_SMALL_PREFETCH;  // sub-chunks in flight per wave
+  // the next sub-chunk's scores are formed while this one's buffer is still
+  // being consumed, so at least two buffers are needed
+  static_assert(P >= 2, "prefetch depth");
+  static constexpr int NQ = 4;    // query rows
+  // keys: a lane holds half a token row
+  static constexpr int HALF = D / 2;
+  static constexpr int KW = HALF * KB / 32;  // words per lane
+  static constexpr int PWK = D * KB / 32;
+  static constexpr int NKI = D / 16;         // MFMAs per key piece (8 coordinates each)
+  static constexpr int KKEYS = 1 << (2 * KB);
+  static constexpr int REPK = KKEYS <= 64 ? 64 : 16;
+  static constexpr int LOGSK = REPK == 64 ? 8 : 6;  // log2(REPK * 4)
+  // values: a lane holds CPL consecutive coordinates of 8 tokens
+  static constexpr int CPL = D / 16;
+  static constexpr int PWV = D * VB / 32;
+  static constexpr int SEGBITS = CPL * VB;  // <= 32 for D <= 128
+  static constexpr int VRAW = (VB == 3) ? 2 : 1;  // a 3-bit segment can cross a word
+  static constexpr int VKEYS = 1 << (2 * VB);
+  static constexpr int REPV = VKEYS <= 64 ? 64 : 16;
+  static constexpr int LOGSV = REPV == 64 ? 9 : 7;  // log2(REPV * 8): (hi pair, lo pair) entries
+  // LDS (bytes): [K hi table][K lo table][V (hi, lo) table][q staging][zeros][row max]
+  static constexpr int KTAB = KKEYS * REPK * 4;
+  static constexpr int VTAB = VKEYS * REPV * 8;
+  static constexpr int LUTK_OFF = 0;
+  static constexpr int LUTV_OFF = 2 * KTAB;
+  static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [p][r][h][i] 8 x f16 = 16 B
+  static constexpr int QST_BYTES = 2 * NQ * 2 * NKI * 16;
+  static constexpr int ZERO_OFF = QST_OFF + QST_BYTES;  // 16 zero bytes
+  static constexpr int QY_OFF = ZERO_OFF + 16;          // [NQ][D] f32 rotated queries
+  static constexpr int QMAX_OFF = QY_OFF + NQ * D * 4;  // [NQ] f32
+  static constexpr int LOOP_BYTES = QMAX_OFF + 16;
+  // epilogue (after a barrier the loop's buffers are dead)
+  static constexpr int WO_OFF = 0;                       // [NW][NQ][D] f32
+  static constexpr int WM_OFF = WO_OFF + NW * NQ * D * 4;  // [NW][NQ]
+  static constexpr int WL_OFF = WM_OFF + NW * NQ * 4;
+  static constexpr int FO_OFF = WL_OFF + NW * NQ * 4;      // [NQ][D] final rows
+  static constexpr int FL_OFF = FO_OFF + NQ * D * 4;       // [NQ] l, [NQ] m
+  static constexpr int FLAG_OFF = FL_OFF + 2 * NQ * 4;
+  static constexpr int POST_BYTES = FLAG_OFF + 16;
+  static constexpr int BYTES = LOOP_BYTES > POST_BYTES ? LOOP_BYTES : POST_BYTES;
+  static_assert(D == 64 || D == 128, "small row-group kernel: head dim 64 or 128");
+  static_assert(KW * 32 == HALF * KB, "key half rows are whole words");
+  static_assert(SEGBITS <= 32, "value segment in one word");
+  static_assert(BYTES <= 160 * 1024, "LDS per workgroup");
+  static_assert(LUTV_OFF < 65536, "table offsets fit the instruction offset field");
+};
+
+// x of lane n - K (mod 16) of its 16-lane row: DPP row_ror:K (so row_ror:12
+// reads lane n + 4).
+template <int K>
+__device__ __forceinline__ uint32_t row_ror_u(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x120 + K, 0xf, 0xf, true));
+}
+
+// Element i of an MFMA result copied into a register of its own.  A DPP
+// operation folded into its user (v_add_f32_dpp) otherwise reads the tuple's
+// first register for every element: the fold drops the sub-register index.
+__device__ __forceinline__ float own_reg(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const h2_t v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Unnormalised Walsh-Hadamard transform of a D-vector held by one wave as
+// y[e] = x[lane + 64 e]: butterflies across e in-lane, across lanes by xor
+// shuffles.
+template <int D>
+__device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], int lane) {
+  constexpr int E = D / kWave;
+#pragma unroll
+  for (int s = E / 2; s >= 1; s >>= 1)
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if ((e & s) == 0) {
+        const float a = y[e], b = y[e + s];
+        y[e] = a + b;
+        y[e + s] = a - b;
+      }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    const float sg = (lane & s) ? -1.f : 1.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) y[e] = fmaf(sg, y[e], __shfl_xor(y[e], s, kWave));
+  }
+}
+
+template <int D, int KB, int VB>
+__global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
+  using S = SmallShape<D, KB, VB>;
+  constexpr int NW = S::NW;
+  constexpr int NT = S::NT;
+  constexpr int SUB = S::SUB;
+  constexpr int P = S::P;
+  constexpr int NQ = S::NQ;
+  constexpr int KW = S::KW;
+  constexpr int NKI = S::NKI;
+  constexpr int CPL = S::CPL;
+  constexpr int VRAW = S::VRAW;
+  constexpr int PWK = S::PWK;
+  constexpr int PWV = S::PWV;
+  constexpr int QE = D / kWave;  // query elements per lane
+
+  __shared__ __align__(16) unsigned char lds[S::BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int split = blockIdx.x;
+  const int gk = blockIdx.y;
+  const int b = blockIdx.z;
+  RowSet rs;
+  rs.init(p, b, gk, 0, NQ);
+
+  int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
+  if (Tb > p.T) Tb = p.T;
+  const int64_t t_begin64 = static_cast<int64_t>(split) * p.chunk;
+  const bool dense = p.rot_kind == TQ_ROT_DENSE;
+  if (t_begin64 >= Tb) {
+    // No tokens for this split (it takes no part in the merge).  An empty
+    // sequence still needs its output: split 0 writes zeros (the reference
+    // divides a zero sum by 1e-6).
+    if (Tb <= 0 && split == 0)
+      for (int idx = tid; idx < NQ * D; idx += NT)
+        if (rs.valid(idx / D)) store_out(p.out, p.q_dtype, rs.qoff(idx / D) * D + idx % D, 0.f);
+    return;
+  }
+  const int t_begin = static_cast<int>(t_begin64);
+  const int t_end = static_cast<int>(Tb < t_begin64 + p.chunk ? Tb : t_begin64 + p.chunk);
+  const int nvalid = static_cast<int>((Tb + p.chunk - 1) / p.chunk);
+  const bool nf16 = p.norm_dtype == TQ_DTYPE_F16;
+
+  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap;
+  const uint32_t tn = static_cast<uint32_t>(t_end);
+  const uint32_t nb = nf16 ? 2u : 4u;
+  const auto krs = buffer_rsrc(static_cast<const char*>(p.k) + kvrow0 * (PWK * 4), tn * (PWK * 4));
+  const auto vrs = buffer_rsrc(static_cast<const char*>(p.v) + kvrow0 * (PWV * 4), tn * (PWV * 4));
+  const auto knrs = buffer_rsrc(static_cast<const char*>(p.kn) + kvrow0 * nb, tn * nb);
+  const auto vnrs = buffer_rsrc(static_cast<const char*>(p.vn) + kvrow0 * nb, tn * nb);
+
+  // ---- lane roles
+  const int jq = (n >> 2) & 1;  // token subset of this lane's score column
+  const int rq = n & 3;         // query row of this lane's score column
+  // keys: token 16 (g >> 1) + n, half g & 1
+  const uint32_t k_lane = (16 * (g >> 1) + n) * (PWK * 4) + (g & 1) * (KW * 4);
+  // norms: tokens 16 jq + 4 g .. + 3 of the sub-chunk
+  const uint32_t n_lane = (16 * jq + 4 * g) * nb;
+  // values: coordinates CPL n .. CPL n + CPL - 1 of tokens 4g + e, 16 + 4g + e
+  const int vbit = CPL * n * VB;
+  const uint32_t v_lane = (vbit >> 5) * 4;
+  const int vsh = vbit & 31;
+  const uint32_t lutk_lane = (lane % S::REPK) * 4;
+  const uint32_t lutv_lane = (lane % S::REPV) * 8;
+  uint32_t kmask = (S::KKEYS - 1u) << S::LOGSK;
+  uint32_t vmask = (S::VKEYS - 1u) << S::LOGSV;
+  asm volatile("" : "+s"(kmask), "+s"(vmask));
+
+  const int n_tok = t_end - t_begin;
+  const int n_my = n_tok > wave * SUB ? (n_tok - wave * SUB + NW * SUB - 1) / (NW * SUB) : 0;
+  auto sub_start = [&](int i) -> int { return t_begin + (i * NW + wave) * SUB; };
+
+  struct Buf {
+    uint32_t k[KW];
+    uint32_t nk[4], nv[4];
+    uint32_t v[8][VRAW];
+  };
+  auto load_sub = [&](Buf& bf, int s0) {
+    const uint32_t t0 = static_cast<uint32_t>(s0);
+    load_words<KW>(bf.k, krs, t0 * (PWK * 4) + k_lane);
+    // 4 norms: 16 bytes (f32) or 8 bytes (f16, the upper two words unused);
+    // one load shape for both keeps the buffers in registers
+    const uint32_t no = t0 * nb + n_lane;
+    const auto a = __builtin_amdgcn_raw_buffer_load_b128(knrs, no, 0, 0);
+    const auto c = __builtin_amdgcn_raw_buffer_load_b128(vnrs, no, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      bf.nk[e] = a[e];
+      bf.nv[e] = c[e];
+    }
+    const uint32_t vo = t0 * (PWV * 4) + v_lane;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
+      load_words<VRAW>(bf.v[e], vrs, vo + tok * (PWV * 4));
+    }
+  };
+  auto norm4 = [&](const uint32_t (&raw)[4], float (&x)[4]) {
+    if (nf16) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        x[e] = f16_bits_to_f32(static_cast<uint16_t>(raw[e >> 1] >> (16 * (e & 1))));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = __builtin_bit_cast(float, raw[e]);
+    }
+  };
+
+  // ---- prologue loads first (query row of this wave, signs, codebooks), then
+  // the pipeline's sub-chunks (loads complete in order)
+  const int qrow = wave;  // waves 0..NQ-1 rotate one query row each
+  const bool qok = qrow < NQ && rs.valid(qrow);
+  uint32_t qraw[QE];
+  float sgn[QE];
+  {
+    const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
+    const int64_t qb = !qok ? 0
+                       : dense ? rs.qoff(qrow) * D
+                               : b * p.q_sb + static_cast<int64_t>(rs.head(qrow)) * p.q_sh +
+                                     static_cast<int64_t>(rs.lpos(qrow)) * p.q_sl;
+    const void* qsrc = dense ? static_cast<const void*>(p.qrot) : p.q;
+#pragma unroll
+    for (int e = 0; e < QE; ++e) {
+      const int64_t i = qb + lane + e * kWave;
+      qraw[e] = !qok ? 0u : q32 ? static_cast<const uint32_t*>(qsrc)[i] : static_cast<const uint16_t*>(qsrc)[i];
+      sgn[e] = dense ? 1.f : p.krot[lane + e * kWave];
+    }
+  }
+  float ckb[1 << KB], cvb[1 << VB];
+#pragma unroll
+  for (int i = 0; i < (1 << KB); ++i) ckb[i] = p.kcb[i];
+#pragma unroll
+  for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
+  Buf buf[P];
+#pragma unroll
+  for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
+
+  // ---- pair tables: hi and lo f16 parts of (c[a] * s, c[b] * s) for key
+  // a | b << bits: keys as a hi table and a lo table of 4-byte entries, values
+  // as one table of 8-byte (hi pair, lo pair) entries.  A thread writes 8
+  // consecutive replicas of one key with 16-byte stores (lanes write
+  // consecutive chunks).
+  float kmax = 0.f, vmax = 0.f;
+#pragma unroll
+  for (int i = 0; i < (1 << KB); ++i) kmax = fmaxf(kmax, fabsf(ckb[i]));
+#pragma unroll
+  for (int i = 0; i < (1 << VB); ++i) vmax = fmaxf(vmax, fabsf(cvb[i]));
+  const float sk = f16_split_scale(kmax);
+  const float cbs_v = f16_split_scale(vmax);
+  auto build_table = [&](uint32_t off, int nkeys, int rep, int bits, const float* cb, float sc,
+                         bool pairs) {
+    const int chunks = rep / 8;
+    for (int slot = tid; slot < nkeys * chunks; slot += NT) {
+      const int key = slot / chunks;
+      uint32_t h0, l0, h1, l1;
+      split_f16(cb[key & ((1 << bits) - 1)] * sc, h0, l0);
+      split_f16(cb[key >> bits] * sc, h1, l1);
+      const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+      if (pairs) {
+        uint4* d = reinterpret_cast<uint4*>(lds + off) + slot * 4;
+        d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
+      } else {
+        uint4* dh = reinterpret_cast<uint4*>(lds + off) + slot * 2;
+        uint4* dl = reinterpret_cast<uint4*>(lds + off + nkeys * rep * 4) + slot * 2;
+        dh[0] = dh[1] = make_uint4(hi, hi, hi, hi);
+        dl[0] = dl[1] = make_uint4(lo, lo, lo, lo);
+      }
+    }
+  };
+  build_table(S::LUTK_OFF, S::KKEYS, S::REPK, KB, p.kcb, sk, false);
+  build_table(S::LUTV_OFF, S::VKEYS, S::REPV, VB, p.vcb, cbs_v, true);
+  if (tid < 4) reinterpret_cast<uint32_t*>(lds + S::ZERO_OFF)[tid] = 0u;
+
+  // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
+  // (dense: rotated by qprep_kernel), into LDS with the row's max |y|
+  if (wave < NQ) {
+    float y[QE];
+    const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
+#pragma unroll
+    for (int e = 0; e < QE; ++e) {
+      const uint32_t raw = qraw[e];
+      const float qv = q32 ? __builtin_bit_cast(float, raw)
+                           : (p.q_dtype == TQ_DTYPE_F16 ? f16_bits_to_f32(static_cast<uint16_t>(raw))
+                                                        : bf16_bits_to_f32(static_cast<uint16_t>(raw)));
+      y[e] = dense ? qv : round_q(p.q_dtype, qv * p.scale_q) * sgn[e];
+    }
+    if (!dense) {
+      wave_fwht<D>(y, lane);
+#pragma unroll
+      for (int e = 0; e < QE; ++e) y[e] *= p.rscale;
+    }
+    float m = 0.f;
+    float* qy = reinterpret_cast<float*>(lds + S::QY_OFF) + wave * D;
+#pragma unroll
+    for (int e = 0; e < QE; ++e) {
+      qy[lane + e * kWave] = y[e];
+      m = fmaxf(m, fabsf(y[e]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    if (lane == 0) reinterpret_cast<float*>(lds + S::QMAX_OFF)[wave] = m;
+  }
+  lds_barrier();
+  // query pieces in B-operand order: staging [p][r][h][i] holds
+  // q_p,r[h D/2 + 8 i + e], e = 0..7, as f16 (one hi/lo scale for all rows)
+  const float* qmaxs = reinterpret_cast<const float*>(lds + S::QMAX_OFF);
+  const float sq = f16_split_scale(fmaxf(fmaxf(qmaxs[0], qmaxs[1]), fmaxf(qmaxs[2], qmaxs[3])));
+  for (int idx = tid; idx < NQ * D; idx += NT) {
+    const int r = idx / D;
+    const int c = idx % D;
+    uint32_t hi, lo;
+    split_f16(reinterpret_cast<const float*>(lds + S::QY_OFF)[idx] * sq, hi, lo);
+    const int h = c / (D / 2);
+    const int i = (c % (D / 2)) / 8;
+    const int e = c % 8;
+    uint16_t* st = reinterpret_cast<uint16_t*>(lds + S::QST_OFF);
+    st[(((0 * NQ + r) * 2 + h) * NKI + i) * 8 + e] = static_cast<uint16_t>(hi);
+    st[(((1 * NQ + r) * 2 + h) * NKI + i) * 8 + e] = static_cast<uint16_t>(lo);
+  }
+  lds_barrier();
+  // B operands: lane (column n = 8 p + 4 jq + rq, g) -- zero unless lane
+  // group g holds tokens of subset jq
+  u32x4_t qb[NKI];
+  {
+    const int pc = n >> 3;
+    const bool on = (g >> 1) == jq;
+    const uint32_t base = S::QST_OFF + (((pc * NQ + rq) * 2 + (g & 1)) * NKI) * 16;
+#pragma unroll
+    for (int i = 0; i < NKI; ++i)
+      qb[i] = lds_at<u32x4_t>(lds, on ? base + i * 16 : static_cast<uint32_t>(S::ZERO_OFF));
+  }
+  // score scale: S * ||k|| * log2(e) / (s_K s_Q) in log2 units
+  const float kscale = 1.4426950408889634f / (sk * sq);
+  // causal limit of this lane's row (keys t <= lim are visible)
+  const bool rq_ok = rs.valid(rq);
+  const int lim = (p.causal && rq_ok) ? static_cast<int>(Tb - p.L + rs.lpos(rq)) : INT32_MAX;
+  int lim_min = INT32_MAX;
+  for (int r = 0; r < NQ; ++r)
+    if (p.causal && rs.valid(r)) lim_min = min(lim_min, static_cast<int>(Tb - p.L + rs.lpos(r)));
+
+  // ------------------------------------------------------------ streaming ----
+  constexpr float kLazy = 7.f;
+  f32x4_t O[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) O[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_row = -INFINITY;  // reference max of this lane's row (log2 units)
+  int E = -1000;            // value-norm exponent of the wave (max ||v|| <= 2^E when set)
+  float vsc = 0.f;          // 2^-E
+  float nv_lim = 0.f;       // 2^(E + 8): larger norms could overflow an f16 weight
+  float l_acc = 0.f;        // sum of p over this lane's tokens
+
+  // two independent accumulator chains (key hi parts, key lo parts)
+  auto scores = [&](const Buf& bf) -> f32x4_t {
+    f32x4_t Ch = {0.f, 0.f, 0.f, 0.f}, Cl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NKI; ++i) {
+      u32x4_t ah, al;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t a = key_addr<2 * KB, S::LOGSK>(bf.k, (8 * i + 2 * u) * KB, lutk_lane, kmask);
+        ah[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + a);
+        al[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
+      }
+      Ch = mfma_f16(ah, qb[i], Ch);
+      Cl = mfma_f16(al, qb[i], Cl);
+    }
+    return Ch + Cl;
+  };
+
+  auto finish = [&](const Buf& bf, f32x4_t C, int s0) {
+    // ---- value operands first (they do not depend on the softmax, and the
+    // slow-path branch below would otherwise keep their table reads behind
+    // it): pairs (4g, 4g+1), (4g+2, 4g+3), (16+4g, ..) of coordinate CPL n + c
+    constexpr uint32_t MEVEN = [] {
+      uint32_t m = 0;
+      for (int j = 0; j < CPL; j += 2) m |= ((1u << VB) - 1u) << (j * VB);
+      return m;
+    }();
+    uint32_t zl[4], zh[4];
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      uint32_t xa, xb;
+      if constexpr (VRAW == 2) {
+        xa = __builtin_amdgcn_alignbit(bf.v[2 * e2][1], bf.v[2 * e2][0], vsh);
+        xb = __builtin_amdgcn_alignbit(bf.v[2 * e2 + 1][1], bf.v[2 * e2 + 1][0], vsh);
+      } else if constexpr (S::SEGBITS < 32) {
+        xa = bf.v[2 * e2][0] >> vsh;
+        xb = bf.v[2 * e2 + 1][0] >> vsh;
+      } else {
+        xa = bf.v[2 * e2][0];
+        xb = bf.v[2 * e2 + 1][0];
+      }
+      zl[e2] = (xa & MEVEN) | ((xb << VB) & ~MEVEN);
+      zh[e2] = ((xa >> VB) & MEVEN) | (xb & ~MEVEN);
+    }
+    uint2 vop[CPL][4];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const uint32_t z[1] = {(c & 1) ? zh[e2] : zl[e2]};
+        vop[c][e2] = lds_at<uint2>(lds, S::LUTV_OFF + key_addr<2 * VB, S::LOGSV>(z, (c >> 1) * 2 * VB, lutv_lane, vmask));
+      }
+    float nk[4], nv[4], sc[4], d[4];
+    norm4(bf.nk, nk);
+    norm4(bf.nv, nv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ci = own_reg(C[i]);
+      sc[i] = ci + __builtin_bit_cast(float, row_ror_u<8>(__builtin_bit_cast(uint32_t, ci)));
+      d[i] = fmaf(sc[i], nk[i] * kscale, -m_row);
+    }
+    const float dmax = fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3]));
+    const float nvmax = fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3]));
+    const bool edge = s0 + SUB > t_end || s0 + SUB - 1 > lim_min;  // wave-uniform
+    if (edge || __any((dmax > kLazy || nvmax > nv_lim) ? 1 : 0)) {
+      // ---- slow path: masks, new reference max / norm exponent, rescale
+      const int tbase = s0 + 16 * jq + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] *= nk[i] * kscale;
+        if (edge) {
+          if (tbase + i > lim) sc[i] = -FLT_MAX;
+          if (tbase + i >= t_end) sc[i] = -INFINITY;
+        }
+      }
+      float rm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      rm = fmaxf(rm, __builtin_bit_cast(float, row_ror_u<4>(__builtin_bit_cast(uint32_t, rm))));
+      rm = fmaxf(rm, __builtin_bit_cast(float, row_ror_u<8>(__builtin_bit_cast(uint32_t, rm))));
+      rm = fmaxf(rm, __shfl_xor(rm, 16, kWave));
+      rm = fmaxf(rm, __shfl_xor(rm, 32, kWave));  // max of this lane's row over the sub-chunk
+      float vm = nvmax;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) vm = fmaxf(vm, __shfl_xor(vm, off, kWave));
+      int ev;
+      frexpf(vm, &ev);
+      const int e2 = ev > E ? ev : E;
+      const float mn = (rm > m_row + kLazy || m_row == -INFINITY) ? fmaxf(m_row, rm) : m_row;
+      // l scales by 2^(m_old - m_new), O also by 2^(E_old - E_new); both
+      // start at zero (the first sub-chunk has m_old = -inf)
+      const float am = (m_row == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_row - mn);
+      const float ao = am * ldexpf(1.f, E - e2);
+      l_acc *= am;
+      float ar[NQ];
+#pragma unroll
+      for (int r = 0; r < NQ; ++r) ar[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ao), r));
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int r = 0; r < NQ; ++r) O[c][r] *= ar[r];
+      m_row = mn;
+      E = e2;
+      vsc = ldexpf(1.f, -E);
+      nv_lim = ldexpf(1.f, E + 8);
+      // masked keys (-FLT_MAX) get weight 1 when their whole row is masked
+      // (m = -FLT_MAX), else 0; keys past the end (-inf) always 0
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = sc[i] - m_row;
+    }
+    float w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pe = __builtin_amdgcn_exp2f(d[i]);
+      l_acc += pe;
+      w[i] = pe * (nv[i] * vsc);
+    }
+    // ---- weights to the A operands: own 4 tokens (subset 0), then those of
+    // lane n + 4 (subset 1); each pair twice, against the (hi pair, lo pair)
+    // k slots of the value operand
+    const uint32_t w01 = pack_f16x2(w[0], w[1]);
+    const uint32_t w23 = pack_f16x2(w[2], w[3]);
+    const uint32_t x01 = row_ror_u<12>(w01);
+    const uint32_t x23 = row_ror_u<12>(w23);
+    const u32x4_t A0 = {w01, w01, w23, w23};
+    const u32x4_t A1 = {x01, x01, x23, x23};
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      O[c] = mfma_f16(A0, u32x4_t{vop[c][0].x, vop[c][0].y, vop[c][1].x, vop[c][1].y}, O[c]);
+      O[c] = mfma_f16(A1, u32x4_t{vop[c][2].x, vop[c][2].y, vop[c][3].x, vop[c][3].y}, O[c]);
+    }
+  };
+
+  // Loads are issued unconditionally (past t_end they read zeros for free),
+  // so the count of outstanding loads is exact for every sub-chunk.
+  f32x4_t Cn;
+  if (n_my > 0) Cn = scores(buf[0]);
+  for (int base = 0; base < n_my; base += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const int i = base + s;
+      if (i < n_my) {
+        const f32x4_t C = Cn;
+        finish(buf[s], C, sub_start(i));
+        if (i + 1 < n_my) Cn = scores(buf[(s + 1) % P]);
+      }
+      load_sub(buf[s], sub_start(i + P));
+    }
+  }
+
+  // --------------------------------------------------- combine the waves ----
+  // l of row r: lanes (g', n) with n < 8 (piece 0), subsets n and n + 4
+  float lr = l_acc + __builtin_bit_cast(float, row_ror_u<12>(__builtin_bit_cast(uint32_t, l_acc)));
+  lr += __shfl_xor(lr, 16, kWave);
+  lr += __shfl_xor(lr, 32, kWave);
+  lds_barrier();  // every wave is done with the tables and staging
+  float* s_wo = reinterpret_cast<float*>(lds + S::WO_OFF);
+  float* s_wm = reinterpret_cast<float*>(lds + S::WM_OFF);
+  float* s_wl = reinterpret_cast<float*>(lds + S::WL_OFF);
+  if (g == 0) {
+    const float oe = ldexpf(1.f, E);  // undo the weights' 2^-E
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      float* dst = s_wo + (wave * NQ + r) * D + CPL * n;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) dst[c] = O[c][r] * oe;
+    }
+    if (n < NQ) {
+      // a wave without tokens keeps m = -inf and contributes nothing
+      s_wm[wave * NQ + n] = m_row;
+      s_wl[wave * NQ + n] = lr;
+    }
+  }
+  lds_barrier();
+  float* s_fo = reinterpret_cast<float*>(lds + S::FO_OFF);
+  float* s_fl = reinterpret_cast<float*>(lds + S::FL_OFF);
+  const float oscale = 1.f / cbs_v;
+  for (int idx = tid; idx < NQ * D; idx += NT) {
+    const int r = idx / D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w * NQ + r]);
+    float a = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wm = s_wm[w * NQ + r];
+      const float f = wm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm - M);
+      a = fmaf(s_wo[(w * NQ) * D + idx], f, a);
+      lt = fmaf(s_wl[w * NQ + r], f, lt);
+    }
+    s_fo[idx] = a * oscale;
+    if (idx % D == 0) {
+      s_fl[r] = lt;
+      s_fl[NQ + r] = M;
+    }
+  }
+  lds_barrier();
+
+  if (nvalid > 1) {
+    // this split's partial for attn_merge_kernel: o through R_V^-1 (Hadamard;
+    // it commutes with the merge's weighted sum and normalisation), then
+    // o[r][:] and (m, l) per row with m in natural-log units
+    if (!dense && wave < NQ) {
+      float y[QE];
+#pragma unroll
+      for (int e = 0; e < QE; ++e) y[e] = s_fo[wave * D + lane + e * kWave];
+      wave_fwht<D>(y, lane);
+#pragma unroll
+      for (int e = 0; e < QE; ++e) s_fo[wave * D + lane + e * kWave] = y[e] * p.rscale * p.vrot[lane + e * kWave];
+    }
+    lds_barrier();
+    const int64_t grp = static_cast<int64_t>(b) * p.Hkv + gk;
+    float4* po4 = reinterpret_cast<float4*>(p.po + (grp * p.n_splits + split) * static_cast<int64_t>(NQ) * D);
+    for (int idx = tid; idx < NQ * D / 4; idx += NT) po4[idx] = reinterpret_cast<const float4*>(s_fo)[idx];
+    if (tid < NQ) {
+      float* pm = p.pml + ((grp * p.n_splits + split) * NQ + tid) * 2;
+      pm[0] = s_fl[NQ + tid] * 0.6931471805599453f;
+      pm[1] = s_fl[tid];
+    }
+    return;
+  }
+
+  // ---- finish: o / l (0 when no token is visible), R_V^-1, store
+  if (!dense) {
+    if (wave < NQ && rs.valid(wave)) {
+      const float lt = s_fl[wave];
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      float y[QE];
+#pragma unroll
+      for (int e = 0; e < QE; ++e) y[e] = s_fo[wave * D + lane + e * kWave] * inv;
+      wave_fwht<D>(y, lane);
+      const int64_t qo = rs.qoff(wave) * D;
+#pragma unroll
+      for (int e = 0; e < QE; ++e)
+        store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * p.vrot[lane + e * kWave]);
+    }
+  } else {
+    for (int idx = tid; idx < NQ * D; idx += NT) {
+      const int r = idx / D;
+      const int c = idx % D;
+      if (!rs.valid(r)) continue;
+      const float lt = s_fl[r];
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      float a2 = 0.f;  // x_c = sum_k y_k R[k][c]
+      for (int k2 = 0; k2 < D; ++k2) a2 = fmaf(s_fo[r * D + k2], p.vrot[static_cast<int64_t>(k2) * D + c], a2);
+      store_out(p.out, p.q_dtype, rs.qoff(r) * D + c, a2 * inv);
+    }
+  }
+}
+
+template <int D, int KB, int VB>
+int launch_small(const AttnParams& p, hipStream_t st) {
+  const dim3 grid(p.n_splits, p.Hkv, p.B);
+  hipLaunchKernelGGL((attn_small_kernel<D, KB, VB>), grid, dim3(SmallShape<D, KB, VB>::NT), 0, st, p);
+  return check_launch("attn_small_kernel");
+}
+
+}  // namespace tq

@@ -169,6 +169,18 @@ def test_ragged_verify_causal(device):
     run_case(device, 78, 3, 8, 2, 4, 900, 128, 2, 1, lengths=[4, 900, 517], causal=True)
 
 
+def test_ragged_verify_small_row_groups(device):
+    """Ragged causal verify with 4 query rows per kv head (GQA 2 x 2 drafts)."""
+    run_case(device, 79, 3, 4, 2, 2, 2600, 128, 3, 3, lengths=[4, 2600, 517], causal=True)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_split_with_fully_masked_rows(device, d):
+    """T = 9 * 256 + 2 with 4 causal drafts: the last split holds 2 keys that rows 0 and 1
+    may not see, so those rows' partials carry only masked scores."""
+    run_case(device, 80 + d, 1, 2, 2, 4, 9 * 256 + 2, d, 3, 3, causal=True)
+
+
 def test_empty_cache_gives_zeros(device):
     q = torch.randn(1, 8, 1, 128, dtype=torch.bfloat16, device=device)
     kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)
