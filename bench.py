@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE / WRITE_SIZE passes over this script scaled by the counters' reading
 # of torch's f32 -> f16 copy of known size (read x 1.9996, write x 0.9999); the
 # counter runs and the calibration are summarised with the committed profiles.
-CFG1_TRAFFIC_BYTES = 28_889_000
+CFG1_TRAFFIC_BYTES = 28_820_702
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 CFG1 = dict(B=1, Hq=32, Hkv=8, D=128, T=32768, bits=3)
 # config 2: ragged batched decode, d=256, K4/V2, dense 256x256 rotation
@@ -113,7 +113,7 @@ def graph_timed(torch, step, steps, warmup, dev):
 def bench_decode(torch, args, dev):
     from kaplumba_amd import ops
 
-    c = CFG1
+    c = dict(CFG1, T=args.tokens)
     per_layer = algorithmic_decode_bytes(c["Hkv"], c["T"], c["D"], c["bits"], c["bits"], 4)
     n_layers = max(2, math.ceil(args.rotate_mb * 1e6 / per_layer))
     layers, kc, vc = make_layer_caches(torch, n_layers, c, dev)
@@ -396,6 +396,9 @@ def main():
     ap.add_argument("--rotate-mb", type=float, default=600.0,
                     help="total size of distinct caches walked by successive steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--tokens", type=int, default=CFG1["T"],
+                    help="cached tokens per kv head of the headline decode leg (context-length "
+                         "sweeps; the config-1 figure is quoted at the default 32768)")
     ap.add_argument("--legs", default="cfg0,cfg2,cfg3,cfg4",
                     help="comma-separated extra legs to run after the cfg1 headline "
                          "(cfg0, cfg2, cfg3, cfg4; empty for the headline only)")
@@ -431,7 +434,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "cfg1 decode attention, 3-bit TurboQuant KV, batch 1, 32 q heads / "
                                "8 kv heads, d=128, 32768 tokens, Hadamard rotation, f32 norms",
-                   "tokens": CFG1["T"], "bytes_per_step": dec["bytes"],
+                   "tokens": args.tokens, "bytes_per_step": dec["bytes"],
                    "distinct_layer_caches": dec["n_layers"], "rotated_mb": round(dec["rotate_mb"], 1),
                    "decode_tokens_per_s": round(1e3 / dec["ms_per_step"], 1),
                    "timing": "HIP graph of the timed steps, one replay bracketed by HIP events"},
