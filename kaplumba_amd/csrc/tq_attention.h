@@ -44,6 +44,7 @@ struct AttnParams {
   const int32_t* seq_lens;
   // shape
   int B, Hq, Hkv, L, R, D;
+  int row_head[4], row_lpos[4];  // row r < 4 of a row group: (r / L, r % L)
   int64_t cap, T;  // capacity per (b, kv head); max tokens
   int causal;
   // split-K

@@ -246,6 +246,10 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   p.L = L;
   p.R = Hq / Hkv;
   p.D = dim;
+  for (int r = 0; r < 4; ++r) {
+    p.row_head[r] = r / L;
+    p.row_lpos[r] = r % L;
+  }
   p.cap = capacity;
   p.T = max_tokens;
   p.causal = causal ? 1 : 0;

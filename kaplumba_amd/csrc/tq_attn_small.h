@@ -95,7 +95,9 @@ struct SmallShape {
   static constexpr int WO_OFF = 0;                       // [NW][NQ][D] f32
   static constexpr int WM_OFF = WO_OFF + NW * NQ * D * 4;  // [NW][NQ]
   static constexpr int WL_OFF = WM_OFF + NW * NQ * 4;
-  static constexpr int FO_OFF = WL_OFF + NW * NQ * 4;      // [NQ][D] final rows
+  static constexpr int WE_OFF = WL_OFF + NW * NQ * 4;      // [NW][NQ] 2^E of the wave
+  static constexpr int WF_OFF = WE_OFF + NW * NQ * 4;      // [NW][NQ] combine factors
+  static constexpr int FO_OFF = WF_OFF + NW * NQ * 4;      // [NQ][D] final rows
   static constexpr int FL_OFF = FO_OFF + NQ * D * 4;       // [NQ] l, [NQ] m
   static constexpr int FLAG_OFF = FL_OFF + 2 * NQ * 4;
   static constexpr int POST_BYTES = FLAG_OFF + 16;
@@ -128,11 +130,44 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// The two wave halves exchanged (v_permlane32_swap): .x = x of lane l for
+// l < 32 and of lane l - 32 otherwise, .y = x of lane l + 32 for l < 32 and
+// of lane l otherwise; so op(.x, .y) is the pairwise op of lanes l, l ^ 32.
+__device__ __forceinline__ float2 halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// c[i] for i < 2^NB from a register array, by a select tree over the bits of i.
+template <int NB>
+__device__ __forceinline__ float mux_pick(const float (&c)[1 << NB], int i) {
+  float v[1 << NB];
+#pragma unroll
+  for (int k = 0; k < (1 << NB); ++k) v[k] = c[k];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const bool hi = (i >> b) & 1;
+#pragma unroll
+    for (int k = 0; k < (1 << (NB - 1 - b)); ++k) v[k] = hi ? v[2 * k + 1] : v[2 * k];
+  }
+  return v[0];
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, xor_lane<1>(x));
+  x = fmaxf(x, xor_lane<2>(x));
+  x = fmaxf(x, xor_lane<4>(x));
+  x = fmaxf(x, xor_lane<8>(x));
+  x = fmaxf(x, xor_lane<16>(x));
+  const float2 h = halves(x);
+  return fmaxf(h.x, h.y);
+}
+
 // Unnormalised Walsh-Hadamard transform of a D-vector held by one wave as
-// y[e] = x[lane + 64 e]: butterflies across e in-lane, across lanes by xor
-// shuffles.
+// y[e] = x[lane + 64 e]: butterflies across e in-lane, across lanes by DPP,
+// swizzles and the half swap.  sgn[k] = -1 where lane bit k is set, else 1.
 template <int D>
-__device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], int lane) {
+__device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], const float (&sgn)[6]) {
   constexpr int E = D / kWave;
 #pragma unroll
   for (int s = E / 2; s >= 1; s >>= 1)
@@ -144,10 +179,15 @@ __device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], int lane) {
         y[e + s] = a - b;
       }
 #pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    const float sg = (lane & s) ? -1.f : 1.f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) y[e] = fmaf(sg, y[e], __shfl_xor(y[e], s, kWave));
+  for (int e = 0; e < E; ++e) {
+    float v = y[e];
+    v = fmaf(sgn[0], v, xor_lane<1>(v));
+    v = fmaf(sgn[1], v, xor_lane<2>(v));
+    v = fmaf(sgn[2], v, xor_lane<4>(v));
+    v = fmaf(sgn[3], v, xor_lane<8>(v));
+    v = fmaf(sgn[4], v, xor_lane<16>(v));
+    const float2 h = halves(v);  // lanes < 32: v + v[l + 32]; others: v[l - 32] - v
+    y[e] = fmaf(sgn[5], h.y, h.x);
   }
 }
 
@@ -177,8 +217,11 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   const int split = blockIdx.x;
   const int gk = blockIdx.y;
   const int b = blockIdx.z;
-  RowSet rs;
-  rs.init(p, b, gk, 0, NQ);
+  // rows r < R * L of this kv head's group: query head gk * R + r / L, position r % L
+  const int nrows = p.R * p.L;
+  auto row_qoff = [&](int r) -> int64_t {  // (b * Hq + head) * L + position
+    return (static_cast<int64_t>(b) * p.Hq + gk * p.R + p.row_head[r]) * p.L + p.row_lpos[r];
+  };
 
   int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
   if (Tb > p.T) Tb = p.T;
@@ -190,7 +233,7 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
     // divides a zero sum by 1e-6).
     if (Tb <= 0 && split == 0)
       for (int idx = tid; idx < NQ * D; idx += NT)
-        if (rs.valid(idx / D)) store_out(p.out, p.q_dtype, rs.qoff(idx / D) * D + idx % D, 0.f);
+        if (idx / D < nrows) store_out(p.out, p.q_dtype, row_qoff(idx / D) * D + idx % D, 0.f);
     return;
   }
   const int t_begin = static_cast<int>(t_begin64);
@@ -207,6 +250,9 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   const auto vnrs = buffer_rsrc(static_cast<const char*>(p.vn) + kvrow0 * nb, tn * nb);
 
   // ---- lane roles
+  float lsg[6];  // -1 where lane bit k is set (Hadamard butterflies)
+#pragma unroll
+  for (int k = 0; k < 6; ++k) lsg[k] = (lane >> k) & 1 ? -1.f : 1.f;
   const int jq = (n >> 2) & 1;  // token subset of this lane's score column
   const int rq = n & 3;         // query row of this lane's score column
   // keys: token 16 (g >> 1) + n, half g & 1
@@ -266,15 +312,15 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   // ---- prologue loads first (query row of this wave, signs, codebooks), then
   // the pipeline's sub-chunks (loads complete in order)
   const int qrow = wave;  // waves 0..NQ-1 rotate one query row each
-  const bool qok = qrow < NQ && rs.valid(qrow);
+  const bool qok = qrow < nrows;
   uint32_t qraw[QE];
   float sgn[QE];
   {
     const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
     const int64_t qb = !qok ? 0
-                       : dense ? rs.qoff(qrow) * D
-                               : b * p.q_sb + static_cast<int64_t>(rs.head(qrow)) * p.q_sh +
-                                     static_cast<int64_t>(rs.lpos(qrow)) * p.q_sl;
+                       : dense ? row_qoff(qrow) * D
+                               : b * p.q_sb + static_cast<int64_t>(gk * p.R + p.row_head[qrow]) * p.q_sh +
+                                     static_cast<int64_t>(p.row_lpos[qrow]) * p.q_sl;
     const void* qsrc = dense ? static_cast<const void*>(p.qrot) : p.q;
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
@@ -304,28 +350,34 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   for (int i = 0; i < (1 << VB); ++i) vmax = fmaxf(vmax, fabsf(cvb[i]));
   const float sk = f16_split_scale(kmax);
   const float cbs_v = f16_split_scale(vmax);
-  auto build_table = [&](uint32_t off, int nkeys, int rep, int bits, const float* cb, float sc,
-                         bool pairs) {
-    const int chunks = rep / 8;
-    for (int slot = tid; slot < nkeys * chunks; slot += NT) {
-      const int key = slot / chunks;
-      uint32_t h0, l0, h1, l1;
-      split_f16(cb[key & ((1 << bits) - 1)] * sc, h0, l0);
-      split_f16(cb[key >> bits] * sc, h1, l1);
-      const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
-      if (pairs) {
-        uint4* d = reinterpret_cast<uint4*>(lds + off) + slot * 4;
-        d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
-      } else {
-        uint4* dh = reinterpret_cast<uint4*>(lds + off) + slot * 2;
-        uint4* dl = reinterpret_cast<uint4*>(lds + off + nkeys * rep * 4) + slot * 2;
-        dh[0] = dh[1] = make_uint4(hi, hi, hi, hi);
-        dl[0] = dl[1] = make_uint4(lo, lo, lo, lo);
-      }
-    }
-  };
-  build_table(S::LUTK_OFF, S::KKEYS, S::REPK, KB, p.kcb, sk, false);
-  build_table(S::LUTV_OFF, S::VKEYS, S::REPV, VB, p.vcb, cbs_v, true);
+  // This thread's table entries (at most one key and one value entry) take
+  // their codebook values from the scalar copies (a mux over the index
+  // bits).  Vector loads here would complete only after the cache prefetch
+  // issued above: loads retire in order.
+  static_assert(S::KKEYS * S::REPK / 8 <= NT && S::VKEYS * S::REPV / 8 <= NT, "one table slot per thread");
+  const int kslot = tid < S::KKEYS * S::REPK / 8 ? tid : 0;
+  const int vslot = tid < S::VKEYS * S::REPV / 8 ? tid : 0;
+  const int kkey = kslot / (S::REPK / 8), vkey = vslot / (S::REPV / 8);
+  const float cka = mux_pick<KB>(ckb, kkey & ((1 << KB) - 1)), ckb2 = mux_pick<KB>(ckb, kkey >> KB);
+  const float cva = mux_pick<VB>(cvb, vkey & ((1 << VB) - 1)), cvb2 = mux_pick<VB>(cvb, vkey >> VB);
+  if (tid < S::KKEYS * S::REPK / 8) {
+    uint32_t h0, l0, h1, l1;
+    split_f16(cka * sk, h0, l0);
+    split_f16(ckb2 * sk, h1, l1);
+    const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+    uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + kslot * 2;
+    uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + kslot * 2;
+    dh[0] = dh[1] = make_uint4(hi, hi, hi, hi);
+    dl[0] = dl[1] = make_uint4(lo, lo, lo, lo);
+  }
+  if (tid < S::VKEYS * S::REPV / 8) {
+    uint32_t h0, l0, h1, l1;
+    split_f16(cva * cbs_v, h0, l0);
+    split_f16(cvb2 * cbs_v, h1, l1);
+    const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+    uint4* d = reinterpret_cast<uint4*>(lds + S::LUTV_OFF) + vslot * 4;
+    d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
+  }
   if (tid < 4) reinterpret_cast<uint32_t*>(lds + S::ZERO_OFF)[tid] = 0u;
 
   // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
@@ -342,7 +394,7 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
       y[e] = dense ? qv : round_q(p.q_dtype, qv * p.scale_q) * sgn[e];
     }
     if (!dense) {
-      wave_fwht<D>(y, lane);
+      wave_fwht<D>(y, lsg);
 #pragma unroll
       for (int e = 0; e < QE; ++e) y[e] *= p.rscale;
     }
@@ -353,8 +405,7 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
       qy[lane + e * kWave] = y[e];
       m = fmaxf(m, fabsf(y[e]));
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    m = wave_max(m);
     if (lane == 0) reinterpret_cast<float*>(lds + S::QMAX_OFF)[wave] = m;
   }
   lds_barrier();
@@ -387,13 +438,19 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
       qb[i] = lds_at<u32x4_t>(lds, on ? base + i * 16 : static_cast<uint32_t>(S::ZERO_OFF));
   }
   // score scale: S * ||k|| * log2(e) / (s_K s_Q) in log2 units
-  const float kscale = 1.4426950408889634f / (sk * sq);
+  const float kscale = 1.4426950408889634f * __builtin_amdgcn_rcpf(sk) * __builtin_amdgcn_rcpf(sq);  // powers of two: exact
   // causal limit of this lane's row (keys t <= lim are visible)
-  const bool rq_ok = rs.valid(rq);
-  const int lim = (p.causal && rq_ok) ? static_cast<int>(Tb - p.L + rs.lpos(rq)) : INT32_MAX;
-  int lim_min = INT32_MAX;
-  for (int r = 0; r < NQ; ++r)
-    if (p.causal && rs.valid(r)) lim_min = min(lim_min, static_cast<int>(Tb - p.L + rs.lpos(r)));
+  int lim = INT32_MAX, lim_min = INT32_MAX;
+  if (p.causal) {
+    const int base_lim = static_cast<int>(Tb - p.L);
+#pragma unroll
+    for (int r = 0; r < NQ; ++r)
+      if (r < nrows) {
+        const int lr_ = base_lim + p.row_lpos[r];
+        lim_min = min(lim_min, lr_);
+        if (rq == r) lim = lr_;
+      }
+  }
 
   // ------------------------------------------------------------ streaming ----
   constexpr float kLazy = 7.f;
@@ -484,11 +541,12 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
       float rm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       rm = fmaxf(rm, __builtin_bit_cast(float, row_ror_u<4>(__builtin_bit_cast(uint32_t, rm))));
       rm = fmaxf(rm, __builtin_bit_cast(float, row_ror_u<8>(__builtin_bit_cast(uint32_t, rm))));
-      rm = fmaxf(rm, __shfl_xor(rm, 16, kWave));
-      rm = fmaxf(rm, __shfl_xor(rm, 32, kWave));  // max of this lane's row over the sub-chunk
-      float vm = nvmax;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) vm = fmaxf(vm, __shfl_xor(vm, off, kWave));
+      rm = fmaxf(rm, xor_lane<16>(rm));
+      {
+        const float2 h = halves(rm);
+        rm = fmaxf(h.x, h.y);  // max of this lane's row over the sub-chunk
+      }
+      const float vm = wave_max(nvmax);
       int ev;
       frexpf(vm, &ev);
       const int e2 = ev > E ? ev : E;
@@ -557,48 +615,58 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   // --------------------------------------------------- combine the waves ----
   // l of row r: lanes (g', n) with n < 8 (piece 0), subsets n and n + 4
   float lr = l_acc + __builtin_bit_cast(float, row_ror_u<12>(__builtin_bit_cast(uint32_t, l_acc)));
-  lr += __shfl_xor(lr, 16, kWave);
-  lr += __shfl_xor(lr, 32, kWave);
+  lr += xor_lane<16>(lr);
+  {
+    const float2 h = halves(lr);
+    lr = h.x + h.y;
+  }
   lds_barrier();  // every wave is done with the tables and staging
   float* s_wo = reinterpret_cast<float*>(lds + S::WO_OFF);
   float* s_wm = reinterpret_cast<float*>(lds + S::WM_OFF);
   float* s_wl = reinterpret_cast<float*>(lds + S::WL_OFF);
+  float* s_we = reinterpret_cast<float*>(lds + S::WE_OFF);
+  float* s_wf = reinterpret_cast<float*>(lds + S::WF_OFF);
   if (g == 0) {
-    const float oe = ldexpf(1.f, E);  // undo the weights' 2^-E
 #pragma unroll
     for (int r = 0; r < NQ; ++r) {
       float* dst = s_wo + (wave * NQ + r) * D + CPL * n;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) dst[c] = O[c][r] * oe;
+      for (int c = 0; c < CPL; ++c) dst[c] = O[c][r];
     }
     if (n < NQ) {
       // a wave without tokens keeps m = -inf and contributes nothing
       s_wm[wave * NQ + n] = m_row;
       s_wl[wave * NQ + n] = lr;
+      s_we[wave * NQ + n] = ldexpf(1.f, E);  // undoes the weights' 2^-E
     }
   }
   lds_barrier();
   float* s_fo = reinterpret_cast<float*>(lds + S::FO_OFF);
   float* s_fl = reinterpret_cast<float*>(lds + S::FL_OFF);
-  const float oscale = 1.f / cbs_v;
-  for (int idx = tid; idx < NQ * D; idx += NT) {
-    const int r = idx / D;
+  if (tid < NQ) {  // per row: the waves' log-sum-exp factors, l and the reference m
+    const int r = tid;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w * NQ + r]);
-    float a = 0.f, lt = 0.f;
+    float lt = 0.f;
+    const float oscale = __builtin_amdgcn_rcpf(cbs_v);  // a power of two: exact
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float wm = s_wm[w * NQ + r];
       const float f = wm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm - M);
-      a = fmaf(s_wo[(w * NQ) * D + idx], f, a);
       lt = fmaf(s_wl[w * NQ + r], f, lt);
+      s_wf[w * NQ + r] = f * s_we[w * NQ + r] * oscale;
     }
-    s_fo[idx] = a * oscale;
-    if (idx % D == 0) {
-      s_fl[r] = lt;
-      s_fl[NQ + r] = M;
-    }
+    s_fl[r] = lt;
+    s_fl[NQ + r] = M;
+  }
+  lds_barrier();
+  for (int idx = tid; idx < NQ * D; idx += NT) {
+    const int r = idx / D;
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) a = fmaf(s_wo[(w * NQ) * D + idx], s_wf[w * NQ + r], a);
+    s_fo[idx] = a;
   }
   lds_barrier();
 
@@ -610,7 +678,7 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
       float y[QE];
 #pragma unroll
       for (int e = 0; e < QE; ++e) y[e] = s_fo[wave * D + lane + e * kWave];
-      wave_fwht<D>(y, lane);
+      wave_fwht<D>(y, lsg);
 #pragma unroll
       for (int e = 0; e < QE; ++e) s_fo[wave * D + lane + e * kWave] = y[e] * p.rscale * p.vrot[lane + e * kWave];
     }
@@ -628,14 +696,14 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
 
   // ---- finish: o / l (0 when no token is visible), R_V^-1, store
   if (!dense) {
-    if (wave < NQ && rs.valid(wave)) {
+    if (wave < nrows) {
       const float lt = s_fl[wave];
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
       float y[QE];
 #pragma unroll
       for (int e = 0; e < QE; ++e) y[e] = s_fo[wave * D + lane + e * kWave] * inv;
-      wave_fwht<D>(y, lane);
-      const int64_t qo = rs.qoff(wave) * D;
+      wave_fwht<D>(y, lsg);
+      const int64_t qo = row_qoff(wave) * D;
 #pragma unroll
       for (int e = 0; e < QE; ++e)
         store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * p.vrot[lane + e * kWave]);
@@ -644,12 +712,12 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
     for (int idx = tid; idx < NQ * D; idx += NT) {
       const int r = idx / D;
       const int c = idx % D;
-      if (!rs.valid(r)) continue;
+      if (r >= nrows) continue;
       const float lt = s_fl[r];
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
       float a2 = 0.f;  // x_c = sum_k y_k R[k][c]
       for (int k2 = 0; k2 < D; ++k2) a2 = fmaf(s_fo[r * D + k2], p.vrot[static_cast<int64_t>(k2) * D + c], a2);
-      store_out(p.out, p.q_dtype, rs.qoff(r) * D + c, a2 * inv);
+      store_out(p.out, p.q_dtype, row_qoff(r) * D + c, a2 * inv);
     }
   }
 }
