@@ -143,6 +143,32 @@ int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int 
                  int64_t capacity, int64_t max_tokens, const int32_t* seq_lens, int causal,
                  void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * tq_attention over a left-padded batch: sequence b's tokens are the cache
+ * rows [seq_starts[b], end_b), end_b = seq_lens[b] (or max_tokens when
+ * seq_lens is NULL).  Rows before seq_starts[b] are padding and are never
+ * read; the causal rule counts positions from end_b as in tq_attention.
+ * seq_starts: NULL (no padding) or a device int32 array of B values in
+ * [0, end_b].  A sequence with no tokens gets a zero output.  Every other
+ * argument is as in tq_attention, which is this call with seq_starts NULL.
+ *
+ * Replaces the attention of the reference's continuous-batching caches:
+ * BatchTurboQuantKVCache (tq.py:6082-6309) stores each batch row
+ * left-padded to a common length with `left_padding` per row, as
+ * BatchKVCache does (cache.py:1099-1260), whose make_mask masks keys before
+ * left_padding (cache.py:1195-1198, base.py:24-42).
+ */
+int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                        int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
+                        int kv_kind, int kv_dtype,
+                        const void* k, const void* k_norms, const void* v, const void* v_norms,
+                        int norm_dtype, int k_bits, int v_bits,
+                        const float* k_codebook, const float* v_codebook,
+                        int rot_kind, const float* k_rot, const float* v_rot,
+                        int64_t capacity, int64_t max_tokens, const int32_t* seq_starts,
+                        const int32_t* seq_lens, int causal,
+                        void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,7 @@ from .cache import (  # noqa: F401
     save_prompt_cache,
     trim_prompt_cache,
 )
+from .batch_cache import BatchKVCache, BatchTurboQuantKVCache  # noqa: F401
 from .base import scaled_dot_product_attention  # noqa: F401
 
 __version__ = "0.1.0"

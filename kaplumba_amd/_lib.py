@@ -54,6 +54,16 @@ SIGNATURES = {
         c_int, c_void_p, c_void_p,                             # rot_kind, k_rot, v_rot
         c_int64, c_int64, c_void_p, c_int,                     # capacity, max_tokens, seq_lens, causal
         c_void_p, c_void_p, c_int64, c_void_p]),               # out, workspace, ws bytes, stream
+    "tq_attention_ranged": (c_int, [
+        c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+        c_int64, c_int64, c_int64, c_float,
+        c_int, c_int,
+        c_void_p, c_void_p, c_void_p, c_void_p,
+        c_int, c_int, c_int,
+        c_void_p, c_void_p,
+        c_int, c_void_p, c_void_p,
+        c_int64, c_int64, c_void_p, c_void_p, c_int,           # ..., seq_starts, seq_lens, causal
+        c_void_p, c_void_p, c_int64, c_void_p]),
 }
 
 

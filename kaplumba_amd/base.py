@@ -11,13 +11,19 @@ from typing import Optional
 import torch
 
 from . import ops
+from .batch_cache import BatchKVCache
 from .cache import _mask_is_causal
 
 
 def scaled_dot_product_attention(queries: torch.Tensor, keys, values, cache, scale: float,
                                  mask, sinks: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Route attention by cache type, as models/base.py:160-226 does."""
-    if type(cache).__name__ == "TurboQuantKVCache":
+    """Route attention by cache type, as models/base.py:160-226 does.
+
+    Left-padded batch caches (BatchTurboQuantKVCache, BatchKVCache) attend
+    over each row's tokens ``[left_padding[b], _idx)``; their ``make_mask``
+    returns None / "causal" and the padding is skipped by the kernel.
+    """
+    if type(cache).__name__ in ("TurboQuantKVCache", "BatchTurboQuantKVCache"):
         if sinks is not None:
             raise ValueError("TurboQuant KV cache does not support attention sinks.")
         if queries.shape[-2] == 1:
@@ -28,4 +34,5 @@ def scaled_dot_product_attention(queries: torch.Tensor, keys, values, cache, sca
     if sinks is not None:
         raise NotImplementedError("attention sinks are not supported by the HIP kernels")
     causal = _mask_is_causal(mask, queries.shape[-2])
-    return ops.attention_plain(queries, keys, values, scale, causal)
+    starts = cache._seq_starts(queries.device) if isinstance(cache, BatchKVCache) else None
+    return ops.attention_plain(queries, keys, values, scale, causal, seq_starts=starts)

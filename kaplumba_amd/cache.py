@@ -489,14 +489,24 @@ class KVCache(_BaseCache):
 
 # ---------------------------------------------------------------- masks ----
 def create_causal_mask(N: int, offset: int = 0, window_size: Optional[int] = None,
-                       lengths=None, device=None) -> torch.Tensor:
-    """Boolean (N, offset+N) causal mask (models/base.py create_causal_mask)."""
+                       right_padding=None, left_padding=None, lengths=None,
+                       device=None) -> torch.Tensor:
+    """Boolean causal mask (models/base.py:24-42): (N, offset+N), or
+    (B, 1, N, offset+N) with per-row ``right_padding`` / ``left_padding``
+    (keys ``k < offset+N-right_padding[b]`` and ``k >= left_padding[b]``)
+    or ``lengths`` (keys ``k < lengths[b]``)."""
     rinds = torch.arange(offset + N, device=device)
     linds = torch.arange(offset, offset + N, device=device)[:, None]
     rinds = rinds[None]
     mask = linds >= rinds
     if window_size is not None:
         mask = mask & (linds < rinds + window_size)
+    if right_padding is not None:
+        rp = torch.as_tensor(right_padding, device=device)[:, None, None, None]
+        mask = mask & (rinds < (offset + N) - rp)
+    if left_padding is not None:
+        lp = torch.as_tensor(left_padding, device=device)[:, None, None, None]
+        mask = mask & (lp <= rinds)
     if lengths is not None:
         lengths = torch.as_tensor(lengths, device=device)[:, None, None, None]
         mask = mask & (rinds < lengths)
@@ -603,7 +613,7 @@ def _tree_unflatten(items):
     return fix(root)
 
 
-_ALLOWED_CACHE_CLASSES = {"KVCache", "TurboQuantKVCache"}
+_ALLOWED_CACHE_CLASSES = {"KVCache", "TurboQuantKVCache", "BatchKVCache", "BatchTurboQuantKVCache"}
 
 
 def save_prompt_cache(file_name: str, cache: List[Any], metadata: Dict[str, str] = {}):
@@ -640,18 +650,39 @@ def load_prompt_cache(file_name: str, return_metadata: bool = False, device=None
     info, metadata, classes = _tree_unflatten(list(meta.items()))
     if isinstance(metadata, list) and not metadata:
         metadata = {}
+    from .batch_cache import BatchKVCache, BatchTurboQuantKVCache
+
+    def mse_state(x):
+        ok = isinstance(x, list) and len(x) == 2 and all(isinstance(t, torch.Tensor) for t in x)
+        return TurboQuantMSEState(*x) if ok else None
+
+    def tensor_or_none(x):
+        return x if isinstance(x, torch.Tensor) else None
+
     caches = []
     for i, cls_name in enumerate(classes):
         if cls_name not in _ALLOWED_CACHE_CLASSES:
             raise ValueError(f"Untrusted cache class '{cls_name}' in prompt cache file.")
-        cls = TurboQuantKVCache if cls_name == "TurboQuantKVCache" else KVCache
         st = tree[i] if isinstance(tree, list) and i < len(tree) else []
         ms = info[i]
-        if cls is TurboQuantKVCache:
+        if cls_name == "TurboQuantKVCache":
+            cls = TurboQuantKVCache
             if isinstance(st, list) and len(st) == 2 and all(isinstance(s, list) for s in st):
                 st = (TurboQuantMSEState(*st[0]), TurboQuantMSEState(*st[1]))
             else:
                 st = []
+        elif cls_name in ("BatchTurboQuantKVCache", "BatchKVCache"):
+            # (keys, values, offset, left_padding); absent keys were not saved
+            st = list(st) + [[]] * (4 - len(st)) if isinstance(st, list) else [[]] * 4
+            if cls_name == "BatchTurboQuantKVCache":
+                cls = BatchTurboQuantKVCache
+                st = (mse_state(st[0]), mse_state(st[1]), st[2], st[3])
+            else:
+                cls = BatchKVCache
+                st = (tensor_or_none(st[0]), tensor_or_none(st[1]), st[2], st[3])
+            st = st[:2] + tuple(t.cpu() if isinstance(t, torch.Tensor) else [] for t in st[2:])
+        else:
+            cls = KVCache
         caches.append(cls.from_state(st, ms))
     if return_metadata:
         return caches, metadata

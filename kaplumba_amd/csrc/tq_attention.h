@@ -41,7 +41,8 @@ struct AttnParams {
   int rot_kind;
   const float* krot;
   const float* vrot;
-  const int32_t* seq_lens;
+  const int32_t* seq_lens;    // end of each sequence's tokens (NULL: T)
+  const int32_t* seq_starts;  // first token of each sequence (left padding; NULL: 0)
   // shape
   int B, Hq, Hkv, L, R, D;
   int row_head[4], row_lpos[4];  // row r < 4 of a row group: (r / L, r % L)
@@ -58,6 +59,23 @@ struct AttnParams {
   // output
   void* out;
 };
+
+// Cache rows [start, start + len) of sequence b: the tokens its queries may
+// see.  Kernels address them from a base moved to row `start`, so splits,
+// causal limits and the merge all work on positions relative to it.
+struct SeqWindow {
+  int64_t start, len;
+};
+
+__device__ __forceinline__ SeqWindow seq_window(const AttnParams& p, int b) {
+  int64_t end = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
+  if (end > p.T) end = p.T;  // lengths beyond max_tokens are clipped
+  if (end < 0) end = 0;
+  int64_t start = p.seq_starts ? static_cast<int64_t>(p.seq_starts[b]) : 0;
+  if (start < 0) start = 0;
+  if (start > end) start = end;
+  return SeqWindow{start, end - start};
+}
 
 struct SplitPlan {
   int n_splits, chunk, n_rg, nq;

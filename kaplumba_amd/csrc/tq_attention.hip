@@ -160,15 +160,16 @@ extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, in
                   workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, false), B, Hq, Hkv, L, dim));
 }
 
-extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
-                            int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l,
-                            float scale, int kv_kind, int kv_dtype, const void* k,
-                            const void* k_norms, const void* v, const void* v_norms,
-                            int norm_dtype, int k_bits, int v_bits, const float* k_codebook,
-                            const float* v_codebook, int rot_kind, const float* k_rot,
-                            const float* v_rot, int64_t capacity, int64_t max_tokens,
-                            const int32_t* seq_lens, int causal, void* out, void* workspace,
-                            int64_t workspace_bytes_given, void* stream) {
+extern "C" int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
+                                   int dim, int64_t q_stride_b, int64_t q_stride_h,
+                                   int64_t q_stride_l, float scale, int kv_kind, int kv_dtype,
+                                   const void* k, const void* k_norms, const void* v,
+                                   const void* v_norms, int norm_dtype, int k_bits, int v_bits,
+                                   const float* k_codebook, const float* v_codebook, int rot_kind,
+                                   const float* k_rot, const float* v_rot, int64_t capacity,
+                                   int64_t max_tokens, const int32_t* seq_starts,
+                                   const int32_t* seq_lens, int causal, void* out, void* workspace,
+                                   int64_t workspace_bytes_given, void* stream) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || L < 1 || Hq % Hkv)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bad heads/L (Hq %d, Hkv %d, L %d)", Hq, Hkv, L);
   if (dim != 64 && dim != 128 && dim != 256)
@@ -240,6 +241,7 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
   p.krot = k_rot;
   p.vrot = v_rot;
   p.seq_lens = seq_lens;
+  p.seq_starts = seq_starts;
   p.B = B;
   p.Hq = Hq;
   p.Hkv = Hkv;
@@ -298,4 +300,20 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
     default: hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(kMergeThreads), 0, st, p); break;
   }
   return check_launch("attn_merge_kernel");
+}
+
+extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                            int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l,
+                            float scale, int kv_kind, int kv_dtype, const void* k,
+                            const void* k_norms, const void* v, const void* v_norms,
+                            int norm_dtype, int k_bits, int v_bits, const float* k_codebook,
+                            const float* v_codebook, int rot_kind, const float* k_rot,
+                            const float* v_rot, int64_t capacity, int64_t max_tokens,
+                            const int32_t* seq_lens, int causal, void* out, void* workspace,
+                            int64_t workspace_bytes_given, void* stream) {
+  return tq_attention_ranged(q, q_dtype, B, Hq, Hkv, L, dim, q_stride_b, q_stride_h, q_stride_l,
+                             scale, kv_kind, kv_dtype, k, k_norms, v, v_norms, norm_dtype, k_bits,
+                             v_bits, k_codebook, v_codebook, rot_kind, k_rot, v_rot, capacity,
+                             max_tokens, nullptr, seq_lens, causal, out, workspace,
+                             workspace_bytes_given, stream);
 }

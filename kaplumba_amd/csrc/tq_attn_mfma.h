@@ -294,8 +294,8 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   RowSet rs;
   rs.init(p, b, gk, rg, NQ);
 
-  int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
-  if (Tb > p.T) Tb = p.T;  // lengths beyond max_tokens are clipped
+  const SeqWindow win = seq_window(p, b);
+  const int64_t Tb = win.len;  // token positions below are relative to win.start
   const int64_t t_begin64 = static_cast<int64_t>(split) * p.chunk;
   if (t_begin64 >= Tb) {
     // No tokens for this split.  An empty sequence still needs its output:
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   // Buffer resources over tokens [0, t_end) of this (sequence, kv head) row:
   // tokens at or past t_end read as zeros without touching memory, so the
   // last sub-chunk needs no clamping and prefetches past the end are free.
-  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap;
+  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap + win.start;
   const uint32_t tn = static_cast<uint32_t>(t_end);
   const uint32_t nb = nf16 ? 2u : 4u;
   const auto krs = buffer_rsrc(static_cast<const char*>(p.k) + kvrow0 * (PWK * 4), tn * (PWK * 4));

@@ -138,8 +138,8 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_plain_kernel(Att
   RowSet rs;
   rs.init(p, b, gk, rg, NQ);
 
-  int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
-  if (Tb > p.T) Tb = p.T;
+  const SeqWindow win = seq_window(p, b);
+  const int64_t Tb = win.len;  // token positions below are relative to win.start
   const int64_t t_begin64 = static_cast<int64_t>(split) * p.chunk;
   if (t_begin64 >= Tb) {
     if (Tb <= 0 && split == 0)
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_plain_kernel(Att
   const int nvalid = static_cast<int>((Tb + p.chunk - 1) / p.chunk);
   // buffer resources over tokens [0, t_end) of this (sequence, kv head) row:
   // rows at or past t_end read as zeros
-  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap;
+  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap + win.start;
   const uint32_t tn = static_cast<uint32_t>(t_end);
   const auto krs = buffer_rsrc(static_cast<const char*>(p.k) + kvrow0 * ROWB, tn * ROWB);
   const auto vrs = buffer_rsrc(static_cast<const char*>(p.v) + kvrow0 * ROWB, tn * ROWB);

@@ -223,8 +223,8 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
     return (static_cast<int64_t>(b) * p.Hq + gk * p.R + p.row_head[r]) * p.L + p.row_lpos[r];
   };
 
-  int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
-  if (Tb > p.T) Tb = p.T;
+  const SeqWindow win = seq_window(p, b);
+  const int64_t Tb = win.len;  // token positions below are relative to win.start
   const int64_t t_begin64 = static_cast<int64_t>(split) * p.chunk;
   const bool dense = p.rot_kind == TQ_ROT_DENSE;
   if (t_begin64 >= Tb) {
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   const int nvalid = static_cast<int>((Tb + p.chunk - 1) / p.chunk);
   const bool nf16 = p.norm_dtype == TQ_DTYPE_F16;
 
-  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap;
+  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap + win.start;
   const uint32_t tn = static_cast<uint32_t>(t_end);
   const uint32_t nb = nf16 ? 2u : 4u;
   const auto krs = buffer_rsrc(static_cast<const char*>(p.k) + kvrow0 * (PWK * 4), tn * (PWK * 4));

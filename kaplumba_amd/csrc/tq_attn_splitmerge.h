@@ -40,8 +40,8 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p)
   const int b = blockIdx.z;
   RowSet rs;
   rs.init(p, b, gk, rg, p.nq);
-  int64_t Tb = p.seq_lens ? static_cast<int64_t>(p.seq_lens[b]) : p.T;
-  if (Tb > p.T) Tb = p.T;
+  const SeqWindow win = seq_window(p, b);
+  const int64_t Tb = win.len;  // token positions below are relative to win.start
   const int nvalid = Tb > 0 ? static_cast<int>((Tb + p.chunk - 1) / p.chunk) : 0;
   if (nvalid <= 1) return;  // the partial kernel wrote these rows itself
   const bool dense = p.rot_kind == TQ_ROT_DENSE;

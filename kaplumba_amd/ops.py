@@ -192,11 +192,36 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def _seq_array(x, B: int, device) -> Optional[torch.Tensor]:
+    """(B,) int32 device copy of per-sequence starts / lengths (or None)."""
+    if x is None:
+        return None
+    x = torch.as_tensor(x).to(device=device, dtype=torch.int32).reshape(-1).contiguous()
+    if x.numel() != B:
+        raise ValueError(f"expected {B} per-sequence values, got {x.numel()}")
+    return x
+
+
+def _call_attention(lib, head, seq_starts, seq_lens, tail, what: str) -> None:
+    """tq_attention, or tq_attention_ranged when sequences carry left padding."""
+    lens = seq_lens.data_ptr() if seq_lens is not None else None
+    if seq_starts is None:
+        rc = lib.tq_attention(*head, lens, *tail)
+    else:
+        rc = lib.tq_attention_ranged(*head, seq_starts.data_ptr(), lens, *tail)
+    _lib.check(rc, what)
+
+
 def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.Tensor,
                      v_norms: torch.Tensor, v_idx: torch.Tensor, key_codec: Codec,
                      value_codec: Codec, scale: float, causal: bool,
-                     seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Attention straight from packed K/V state views (B, Hkv, T[, PW])."""
+                     seq_lens: Optional[torch.Tensor] = None,
+                     seq_starts: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention straight from packed K/V state views (B, Hkv, T[, PW]).
+
+    ``seq_lens`` (B,) ends each sequence before T (ragged batches);
+    ``seq_starts`` (B,) skips each sequence's left padding.
+    """
     _require_device(queries, k_norms, k_idx, v_norms, v_idx)
     B, Hq, L, D = queries.shape
     Hkv, T = k_norms.shape[1], k_norms.shape[2]
@@ -216,32 +241,34 @@ def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.
         raise ValueError("key and value buffers must share a capacity")
     if k_norms.dtype != v_norms.dtype:
         raise ValueError("key and value norms must share a dtype")
-    if seq_lens is not None:
-        seq_lens = seq_lens.to(device=queries.device, dtype=torch.int32).contiguous()
+    seq_lens = _seq_array(seq_lens, B, queries.device)
+    seq_starts = _seq_array(seq_starts, B, queries.device)
     out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
     lib = _lib.load()
     wsb = lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T)
     ws = _workspace(queries.device, wsb)
     kt = key_codec.device_tensors(queries.device)
     vt = value_codec.device_tensors(queries.device)
-    rc = lib.tq_attention(
-        queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
-        queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
-        _lib.TQ_KV_PACKED, 0,
-        k_idx.data_ptr(), k_norms.data_ptr(), v_idx.data_ptr(), v_norms.data_ptr(),
-        _lib.torch_dtype_code(k_norms.dtype), key_codec.bits, value_codec.bits,
-        kt["codebook"].data_ptr(), vt["codebook"].data_ptr(), key_codec.rot_kind,
-        kt["rot"].data_ptr(), vt["rot"].data_ptr(), cap, T,
-        seq_lens.data_ptr() if seq_lens is not None else None, 1 if causal else 0,
-        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
-    _lib.check(rc, "tq_attention")
+    head = (queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
+            queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
+            _lib.TQ_KV_PACKED, 0,
+            k_idx.data_ptr(), k_norms.data_ptr(), v_idx.data_ptr(), v_norms.data_ptr(),
+            _lib.torch_dtype_code(k_norms.dtype), key_codec.bits, value_codec.bits,
+            kt["codebook"].data_ptr(), vt["codebook"].data_ptr(), key_codec.rot_kind,
+            kt["rot"].data_ptr(), vt["rot"].data_ptr(), cap, T)
+    tail = (1 if causal else 0, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
+    _call_attention(lib, head, seq_starts, seq_lens, tail, "tq_attention")
     return out
 
 
 def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                     scale: float, causal: bool,
-                    seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Attention over unquantized fp16/bf16 K/V views (B, Hkv, T, D) of (B, Hkv, cap, D)."""
+                    seq_lens: Optional[torch.Tensor] = None,
+                    seq_starts: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention over unquantized fp16/bf16 K/V views (B, Hkv, T, D) of (B, Hkv, cap, D).
+
+    ``seq_lens`` / ``seq_starts`` as in ``attention_packed``.
+    """
     _require_device(queries, keys, values)
     B, Hq, L, D = queries.shape
     Hkv, T = keys.shape[1], keys.shape[2]
@@ -264,18 +291,17 @@ def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Ten
         raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
     if queries.stride(-1) != 1:
         queries = queries.contiguous()
-    if seq_lens is not None:
-        seq_lens = seq_lens.to(device=queries.device, dtype=torch.int32).contiguous()
+    seq_lens = _seq_array(seq_lens, B, queries.device)
+    seq_starts = _seq_array(seq_starts, B, queries.device)
     out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
     lib = _lib.load()
     wsb = lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T)
     ws = _workspace(queries.device, wsb)
-    rc = lib.tq_attention(
-        queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
-        queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
-        _lib.TQ_KV_PLAIN, _lib.torch_dtype_code(keys.dtype),
-        keys.data_ptr(), None, values.data_ptr(), None, 0, 0, 0, None, None, 0, None, None,
-        cap, T, seq_lens.data_ptr() if seq_lens is not None else None, 1 if causal else 0,
-        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
-    _lib.check(rc, "tq_attention(plain)")
+    head = (queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
+            queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
+            _lib.TQ_KV_PLAIN, _lib.torch_dtype_code(keys.dtype),
+            keys.data_ptr(), None, values.data_ptr(), None, 0, 0, 0, None, None, 0, None, None,
+            cap, T)
+    tail = (1 if causal else 0, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
+    _call_attention(lib, head, seq_starts, seq_lens, tail, "tq_attention(plain)")
     return out

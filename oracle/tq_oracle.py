@@ -384,7 +384,8 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
               k_codebook: np.ndarray, v_codebook: np.ndarray, rot_kind: str,
               k_rot: np.ndarray, v_rot: np.ndarray, scale: float, q_dtype: str,
               causal: bool = False, lengths: Optional[Sequence[int]] = None,
-              v_dim: Optional[int] = None) -> np.ndarray:
+              v_dim: Optional[int] = None,
+              starts: Optional[Sequence[int]] = None) -> np.ndarray:
     """TurboQuant attention in float64, ``quantized_attention`` semantics.
 
     Restates :5110-5203 with ``_apply_attention_mask`` (:5079-5108) and the
@@ -394,6 +395,10 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
     ``sum p * n_v * c_v[idx]`` in rotated space; ``R_V^-1``; divide by
     ``max(sum p, 1e-6)``.  ``lengths`` gives per-sequence cache lengths for
     ragged batches (tokens beyond a length do not exist for that sequence).
+    ``starts`` gives per-sequence left padding: keys before it do not exist
+    either, which is the left-padding mask ``left_padding <= k`` of
+    models/base.py:40-41 that BatchKVCache.make_mask applies
+    (models/cache.py:1195-1198); the causal rule still counts from the end.
     Returns float64 (B, Hq, L, Dv); callers round to the query dtype.
     """
     B, Hq, L, D = q.shape
@@ -411,14 +416,16 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
     out = np.zeros((B, Hq, L, Dv), np.float64)
     fmin = float(np.finfo(np.float32).min)
     for b in range(B):
-        T = cap if lengths is None else int(lengths[b])
+        end = cap if lengths is None else int(lengths[b])
+        t0 = 0 if starts is None else min(int(starts[b]), end)
+        T = end - t0
         if T == 0:
             continue
         for g in range(Hkv):
-            kidx = unpack_lowbit(k_packed[b, g, :T], k_bits, D)
-            vidx = unpack_lowbit(v_packed[b, g, :T], v_bits, Dv)
-            kd = kc[kidx] * np.asarray(k_norms[b, g, :T], np.float64)[:, None]
-            vd = vc[vidx] * np.asarray(v_norms[b, g, :T], np.float64)[:, None]
+            kidx = unpack_lowbit(k_packed[b, g, t0:end], k_bits, D)
+            vidx = unpack_lowbit(v_packed[b, g, t0:end], v_bits, Dv)
+            kd = kc[kidx] * np.asarray(k_norms[b, g, t0:end], np.float64)[:, None]
+            vd = vc[vidx] * np.asarray(v_norms[b, g, t0:end], np.float64)[:, None]
             for r in range(R):
                 h = g * R + r
                 s = qr[b, h] @ kd.T                      # (L, T)
@@ -440,12 +447,14 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
 
 def attention_plain(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float,
                     q_dtype: str, causal: bool = False,
-                    lengths: Optional[Sequence[int]] = None) -> np.ndarray:
+                    lengths: Optional[Sequence[int]] = None,
+                    starts: Optional[Sequence[int]] = None) -> np.ndarray:
     """Standard SDPA over an unquantized (fp16/bf16) cache, float64.
 
     The mixed-precision layers of the reference keep model-dtype K/V and call
     ``mx.fast.scaled_dot_product_attention`` (models/base.py:218-226,
-    models/cache.py:55-61).  Queries are scaled in their dtype as above.
+    models/cache.py:55-61).  Queries are scaled in their dtype as above;
+    ``lengths`` and ``starts`` as in ``attention``.
     """
     B, Hq, L, D = q.shape
     Hkv = k.shape[1]
@@ -454,18 +463,20 @@ def attention_plain(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float
     out = np.zeros((B, Hq, L, v.shape[-1]), np.float64)
     fmin = float(np.finfo(np.float32).min)
     for b in range(B):
-        T = k.shape[2] if lengths is None else int(lengths[b])
+        end = k.shape[2] if lengths is None else int(lengths[b])
+        t0 = 0 if starts is None else min(int(starts[b]), end)
+        T = end - t0
         if T == 0:
             continue
         for h in range(Hq):
             g = h // R
-            s = qs[b, h] @ np.asarray(k[b, g, :T], np.float64).T
+            s = qs[b, h] @ np.asarray(k[b, g, t0:end], np.float64).T
             if causal:
                 qi = (T - L) + np.arange(L)[:, None]
                 s = np.where(qi >= np.arange(T)[None, :], s, fmin)
             m = s.max(axis=-1, keepdims=True)
             p = np.exp(s - m)
-            out[b, h] = (p @ np.asarray(v[b, g, :T], np.float64)) / np.maximum(
+            out[b, h] = (p @ np.asarray(v[b, g, t0:end], np.float64)) / np.maximum(
                 p.sum(axis=-1, keepdims=True), float(EPS))
     return out
 

@@ -109,19 +109,23 @@ def build_case(seed, B, Hq, Hkv, L, T, d, kb, vb, rot="hadamard", qdt="bf16", no
 
 
 def run_case(device, seed, B, Hq, Hkv, L, T, d, kb, vb, rot="hadamard", qdt="bf16", causal=None,
-             lengths=None, norm="float32"):
+             lengths=None, norm="float32", starts=None):
     causal = (L > 1) if causal is None else causal
     q, kp, kn, vp, vn, kr, vr = build_case(seed, B, Hq, Hkv, L, T, d, kb, vb, rot, qdt, norm)
     want = O.attention(q, kp, kn, vp, vn, k_bits=kb, v_bits=vb, k_codebook=O.beta_codebook(d, kb),
                        v_codebook=O.beta_codebook(d, vb), rot_kind=rot, k_rot=kr, v_rot=vr,
-                       scale=1 / math.sqrt(d), q_dtype=qdt, causal=causal, lengths=lengths)
+                       scale=1 / math.sqrt(d), q_dtype=qdt, causal=causal, lengths=lengths,
+                       starts=starts)
     nd = torch.float16 if norm == "float16" else torch.float32
     kn_t, ki, vn_t, vi = to_buffers(kp, kn, vp, vn, device, norm_dtype=nd)
     sl = torch.tensor(lengths, dtype=torch.int32, device=device) if lengths is not None else None
     out = ops.attention_packed(q_tensor(q, qdt, device), kn_t, ki, vn_t, vi,
                                ops.Codec(d, kb, 0, rot), ops.Codec(d, vb, 1, rot),
-                               1 / math.sqrt(d), causal, seq_lens=sl)
+                               1 / math.sqrt(d), causal, seq_lens=sl,
+                               seq_starts=None if starts is None else torch.tensor(starts))
     label = f"B{B} Hq{Hq} Hkv{Hkv} L{L} T{T} d{d} k{kb}v{vb} {rot} {qdt}"
+    if starts is not None:
+        label += f" starts{list(starts)}"
     assert_close(out, want, qdt, label)
 
 
