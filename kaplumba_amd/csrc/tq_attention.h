@@ -17,7 +17,11 @@
 
 namespace tq {
 
-constexpr int kMaxChunk = 2048;   // tokens per split
+// Longest split in tokens.  The split count aims at one wave of workgroups
+// over the device, and only that bounds a split's length: every extra
+// round of workgroups repeats the prologue (tables, query rotation) and the
+// epilogue (wave combine, partial write) in series.
+constexpr int kMaxChunk = 1 << 20;
 constexpr int kMaxSplits = 1024;  // splits per sequence
 // The workspace starts with a fixed 64 KiB region the C ABI documents as
 // zero-initialised counters; the current kernels leave it untouched.
@@ -87,6 +91,9 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
 // R <= 4, or verify with R * L <= 4) at head dim 64 / 128 run the small
 // row-group kernel (tq_attn_small.h).
 bool small_rows_path(int kv_kind, int D, int rows);
+// Packed caches at head dim 128 with more rows run 16-row groups on the
+// register-softmax kernel of tq_attn_rows16.h.
+bool rows16_path(int kv_kind, int D, int rows);
 int64_t workspace_bytes(const SplitPlan& p, int B, int Hq, int Hkv, int L, int D);
 
 // Kernel launchers instantiated per head dim in tq_attn_d*.hip.

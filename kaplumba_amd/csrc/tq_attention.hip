@@ -105,6 +105,15 @@ bool small_rows_path(int kv_kind, int D, int rows) {
   return enabled && kv_kind == TQ_KV_PACKED && D <= 128 && rows <= 4;
 }
 
+bool rows16_path(int kv_kind, int D, int rows) {
+  // KAPLUMBA_TQ_ROWS16=0 selects the general kernel instead
+  static const bool enabled = [] {
+    const char* e = getenv("KAPLUMBA_TQ_ROWS16");
+    return !(e && e[0] == '0');
+  }();
+  return enabled && kv_kind == TQ_KV_PACKED && D == 128 && rows > 4;
+}
+
 SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool packed) {
   SplitPlan sp{};
   const int R = Hq / Hkv;
@@ -128,7 +137,13 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
   ns = std::max<int64_t>(1, std::min(ns, max_by_tokens));
   int64_t chunk = (T + ns - 1) / ns;
   chunk = std::max<int64_t>(256, (chunk + 255) / 256 * 256);  // whole sub-chunks for every wave
-  chunk = std::min<int64_t>(chunk, kMaxChunk);
+  // longest split (KAPLUMBA_TQ_MAX_CHUNK overrides, for tuning)
+  static const int max_chunk = [] {
+    const char* e = getenv("KAPLUMBA_TQ_MAX_CHUNK");
+    const int v = e ? atoi(e) : kMaxChunk;
+    return v >= 256 && v <= (1 << 24) ? v / 256 * 256 : kMaxChunk;
+  }();
+  chunk = std::min<int64_t>(chunk, max_chunk);
   sp.chunk = static_cast<int>(chunk);
   sp.n_splits = static_cast<int>(std::max<int64_t>(1, (T + chunk - 1) / chunk));
   return sp;

@@ -1,12 +1,14 @@
 // Kernel dispatch of the split-K attention (included by tq_attn_d*.hip):
-// packed TurboQuant caches go to the matrix-core kernel of tq_attn_mfma.h,
-// plain fp16 / bf16 caches to the one of tq_attn_plain.h.  Both write split
-// partials that attn_merge_kernel combines (a single split is finished in
-// the partial kernel itself).
+// packed TurboQuant caches go to the small row-group kernel (<= 4 rows,
+// d <= 128), the 16-row kernel (d = 128) or the general matrix-core kernel
+// of tq_attn_mfma.h; plain fp16 / bf16 caches to the one of tq_attn_plain.h.
+// Each writes split partials that attn_merge_kernel combines (a single split
+// is finished in the partial kernel itself).
 #pragma once
 
 #include "tq_attn_mfma.h"
 #include "tq_attn_plain.h"
+#include "tq_attn_rows16.h"
 #include "tq_attn_small.h"
 
 namespace tq {
@@ -22,10 +24,24 @@ int launch_small_vb(const AttnParams& p, int vb, hipStream_t st) {
   return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
 }
 
+template <int KB>
+int launch_rows16_vb(const AttnParams& p, int vb, hipStream_t st) {
+  switch (vb) {
+    case 1: return launch_rows16<KB, 1>(p, st);
+    case 2: return launch_rows16<KB, 2>(p, st);
+    case 3: return launch_rows16<KB, 3>(p, st);
+    case 4: return launch_rows16<KB, 4>(p, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
+}
+
 template <int D, int KB>
 int launch_partial_vb(const AttnParams& p, int vb, hipStream_t st) {
   if constexpr (D <= 128) {
     if (small_rows_path(TQ_KV_PACKED, D, p.R * p.L)) return launch_small_vb<D, KB>(p, vb, st);
+  }
+  if constexpr (D == 128) {
+    if (rows16_path(TQ_KV_PACKED, D, p.R * p.L)) return launch_rows16_vb<KB>(p, vb, st);
   }
   switch (vb) {
     case 1: return launch_mfma_nq<D, KB, 1>(p, st);

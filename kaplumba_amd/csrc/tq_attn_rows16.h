@@ -1,0 +1,656 @@
+// TurboQuant verify / prefill / wide-GQA attention for 16-row groups at head
+// dim 128, straight from packed indices: the layout of the small row-group
+// kernel (tq_attn_small.h) with all 16 MFMA columns holding query rows.
+//
+// Workgroup: 8 wave64s own tokens [t_begin, t_end) of one (sequence, kv head)
+// and 16 query rows of its GQA group (row group rg: rows 16 rg .. 16 rg + 15
+// of the R * L rows, row -> (head r / L, position r % L)).  Tokens are cut
+// into 32-token sub-chunks; sub-chunk i belongs to wave i % 8, and each wave
+// keeps the global loads of its next P sub-chunks in flight.
+//
+// Lane roles (l = lane, n = l % 16, g = l / 16):
+//   scores  S^T[tok][row] = sum_d k[tok][d] * q_row[d]   (two 16 x 16 tiles)
+//     A = keys: lane (m, g) holds tokens m and 16 + m, coordinate quarter g
+//         (D/4 coordinates: a contiguous bit span of each packed row); MFMA
+//         j of a tile takes coordinates g D/4 + 8 j .. + 7 of every lane,
+//         hi and lo f16 parts of the codebook values from two tables,
+//     B = queries: lane (row n, g) holds the same coordinates of row n, hi
+//         and lo f16 parts in separate operands.  k_hi q_hi + k_hi q_lo +
+//         k_lo q_hi keeps f32-class accuracy (the dropped k_lo q_lo term is
+//         below 2^-22 relative).
+//     Output: lane (g, row n), register i = token 4g + i of the tile.
+//   softmax per lane: 8 tokens of row n (4 per tile).
+//   values  O[row][d] = sum_tok w[row][tok] * v[tok][d]   (16 x 16 tiles)
+//     A = weights: lane (row n, g) holds tokens 4g .. 4g+3 and 16+4g ..
+//         16+4g+3 as f16 -- exactly its own 8 weights: no transpose,
+//     B = values: as in the small kernel, (hi pair, lo pair) of two tokens
+//         per 8-byte table read against weights (w_a, w_b, w_a, w_b).
+//     Output: lane (g, n), register i = row 4g + i, coordinate (D/16) n + c.
+// Softmax, value-norm exponent, table replication and the split protocol
+// are those of the small kernel; the partials use the row-group layout of
+// attn_merge_kernel (16 rows per group).
+// Semantics: quantized_attention, turboquant_cache.py:5110-5203.
+#pragma once
+
+#include "tq_attn_small.h"
+
+namespace tq {
+
+template <int KB, int VB>
+struct Rows16Shape {
+  static constexpr int D = 128;
+  static constexpr int NW = 8;
+  static constexpr int NT = NW * kWave;
+  static constexpr int SUB = 32;  // tokens per sub-chunk (two 16-token tiles)
+  static constexpr int P = 2;     // sub-chunks in flight per wave
+  static constexpr int NQ = 16;   // query rows
+  // keys: a lane holds a quarter row of two tokens
+  static constexpr int QTR = D / 4;
+  static constexpr int KW = QTR * KB / 32;  // words per token and lane
+  static constexpr int PWK = D * KB / 32;
+  static constexpr int NKJ = D / 32;        // MFMAs per tile and key piece
+  static constexpr int KKEYS = 1 << (2 * KB);
+  static constexpr int REPK = KKEYS <= 64 ? 64 : 16;
+  static constexpr int LOGSK = REPK == 64 ? 8 : 6;  // log2(REPK * 4)
+  // values: a lane holds CPL consecutive coordinates of 8 tokens
+  static constexpr int CPL = D / 16;
+  static constexpr int PWV = D * VB / 32;
+  static constexpr int SEGBITS = CPL * VB;
+  static constexpr int VRAW = (VB == 3) ? 2 : 1;
+  static constexpr int VKEYS = 1 << (2 * VB);
+  static constexpr int REPV = VKEYS <= 64 ? 64 : 16;
+  static constexpr int LOGSV = REPV == 64 ? 9 : 7;
+  // LDS (bytes): [K hi table][K lo table][V (hi, lo) table][q staging][rows][row max]
+  static constexpr int KTAB = KKEYS * REPK * 4;
+  static constexpr int VTAB = VKEYS * REPV * 8;
+  static constexpr int LUTK_OFF = 0;
+  static constexpr int LUTV_OFF = 2 * KTAB;
+  static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [piece][row][g][j] 8 x f16 = 16 B
+  static constexpr int QST_BYTES = 2 * NQ * 4 * NKJ * 16;
+  static constexpr int QY_OFF = QST_OFF + QST_BYTES;    // [NQ][D] f32 rotated queries
+  static constexpr int QMAX_OFF = QY_OFF + NQ * D * 4;  // [NQ] f32
+  static constexpr int LOOP_BYTES = QMAX_OFF + NQ * 4;
+  // epilogue (after a barrier the loop's buffers are dead)
+  static constexpr int WO_OFF = 0;                         // [NW][NQ][D] f32
+  static constexpr int WM_OFF = WO_OFF + NW * NQ * D * 4;  // [NW][NQ]
+  static constexpr int WL_OFF = WM_OFF + NW * NQ * 4;
+  static constexpr int WE_OFF = WL_OFF + NW * NQ * 4;
+  static constexpr int WF_OFF = WE_OFF + NW * NQ * 4;
+  static constexpr int FO_OFF = WF_OFF + NW * NQ * 4;      // [NQ][D] final rows
+  static constexpr int FL_OFF = FO_OFF + NQ * D * 4;       // [NQ] l, [NQ] m
+  static constexpr int POST_BYTES = FL_OFF + 2 * NQ * 4;
+  static constexpr int BYTES = LOOP_BYTES > POST_BYTES ? LOOP_BYTES : POST_BYTES;
+  static_assert(KW * 32 == QTR * KB, "key quarter rows are whole words");
+  static_assert(SEGBITS <= 32, "value segment in one word");
+  static_assert(BYTES <= 160 * 1024, "LDS per workgroup");
+  static_assert(LUTV_OFF < 65536, "table offsets fit the instruction offset field");
+};
+
+template <int KB, int VB>
+__global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
+  using S = Rows16Shape<KB, VB>;
+  constexpr int D = S::D;
+  constexpr int NW = S::NW;
+  constexpr int NT = S::NT;
+  constexpr int SUB = S::SUB;
+  constexpr int P = S::P;
+  constexpr int NQ = S::NQ;
+  constexpr int KW = S::KW;
+  constexpr int NKJ = S::NKJ;
+  constexpr int CPL = S::CPL;
+  constexpr int VRAW = S::VRAW;
+  constexpr int PWK = S::PWK;
+  constexpr int PWV = S::PWV;
+  constexpr int QE = D / kWave;  // query elements per lane
+
+  __shared__ __align__(16) unsigned char lds[S::BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int split = blockIdx.x;
+  const int gk = blockIdx.y / p.n_rg;
+  const int rg = blockIdx.y % p.n_rg;
+  const int b = blockIdx.z;
+  RowSet rs;
+  rs.init(p, b, gk, rg, NQ);
+
+  const SeqWindow win = seq_window(p, b);
+  const int64_t Tb = win.len;  // token positions below are relative to win.start
+  const int64_t t_begin64 = static_cast<int64_t>(split) * p.chunk;
+  const bool dense = p.rot_kind == TQ_ROT_DENSE;
+  if (t_begin64 >= Tb) {
+    // No tokens for this split (it takes no part in the merge); an empty
+    // sequence's rows are zeros, written by split 0.
+    if (Tb <= 0 && split == 0)
+      for (int idx = tid; idx < NQ * D; idx += NT)
+        if (rs.valid(idx / D)) store_out(p.out, p.q_dtype, rs.qoff(idx / D) * D + idx % D, 0.f);
+    return;
+  }
+  const int t_begin = static_cast<int>(t_begin64);
+  const int t_end = static_cast<int>(Tb < t_begin64 + p.chunk ? Tb : t_begin64 + p.chunk);
+  const int nvalid = static_cast<int>((Tb + p.chunk - 1) / p.chunk);
+  const bool nf16 = p.norm_dtype == TQ_DTYPE_F16;
+
+  const int64_t kvrow0 = (static_cast<int64_t>(b) * p.Hkv + gk) * p.cap + win.start;
+  const uint32_t tn = static_cast<uint32_t>(t_end);
+  const uint32_t nb = nf16 ? 2u : 4u;
+  const auto krs = buffer_rsrc(static_cast<const char*>(p.k) + kvrow0 * (PWK * 4), tn * (PWK * 4));
+  const auto vrs = buffer_rsrc(static_cast<const char*>(p.v) + kvrow0 * (PWV * 4), tn * (PWV * 4));
+  const auto knrs = buffer_rsrc(static_cast<const char*>(p.kn) + kvrow0 * nb, tn * nb);
+  const auto vnrs = buffer_rsrc(static_cast<const char*>(p.vn) + kvrow0 * nb, tn * nb);
+
+  // ---- lane roles
+  float lsg[6];  // -1 where lane bit k is set (Hadamard butterflies)
+#pragma unroll
+  for (int k = 0; k < 6; ++k) lsg[k] = (lane >> k) & 1 ? -1.f : 1.f;
+  // keys: tokens n and 16 + n, quarter g
+  const uint32_t k_lane = n * (PWK * 4) + g * (KW * 4);
+  // norms: tokens 4g .. 4g + 3 of each tile
+  const uint32_t n_lane = 4 * g * nb;
+  // values: coordinates CPL n .. CPL n + CPL - 1 of tokens 4g + e, 16 + 4g + e
+  const int vbit = CPL * n * VB;
+  const uint32_t v_lane = (vbit >> 5) * 4;
+  const int vsh = vbit & 31;
+  const uint32_t lutk_lane = (lane % S::REPK) * 4;
+  const uint32_t lutv_lane = (lane % S::REPV) * 8;
+  uint32_t kmask = (S::KKEYS - 1u) << S::LOGSK;
+  uint32_t vmask = (S::VKEYS - 1u) << S::LOGSV;
+  asm volatile("" : "+s"(kmask), "+s"(vmask));
+
+  const int n_tok = t_end - t_begin;
+  const int n_my = n_tok > wave * SUB ? (n_tok - wave * SUB + NW * SUB - 1) / (NW * SUB) : 0;
+  auto sub_start = [&](int i) -> int { return t_begin + (i * NW + wave) * SUB; };
+
+  struct Buf {
+    uint32_t k[2][KW];
+    uint32_t nk[2][4], nv[2][4];
+    uint32_t v[8][VRAW];
+  };
+  auto load_sub = [&](Buf& bf, int s0) {
+    const uint32_t t0 = static_cast<uint32_t>(s0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) load_words<KW>(bf.k[t], krs, (t0 + 16 * t) * (PWK * 4) + k_lane);
+    // 4 norms per tile: 16 bytes (f32) or 8 bytes (f16, the upper two words
+    // unused); one load shape for both keeps the buffers in registers
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t no = (t0 + 16 * t) * nb + n_lane;
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(knrs, no, 0, 0);
+      const auto c = __builtin_amdgcn_raw_buffer_load_b128(vnrs, no, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf.nk[t][e] = a[e];
+        bf.nv[t][e] = c[e];
+      }
+    }
+    const uint32_t vo = t0 * (PWV * 4) + v_lane;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
+      load_words<VRAW>(bf.v[e], vrs, vo + tok * (PWV * 4));
+    }
+  };
+  auto norm4 = [&](const uint32_t (&raw)[4], float (&x)[4]) {
+    if (nf16) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        x[e] = f16_bits_to_f32(static_cast<uint16_t>(raw[e >> 1] >> (16 * (e & 1))));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = __builtin_bit_cast(float, raw[e]);
+    }
+  };
+
+  // ---- prologue loads first (this wave's two query rows, signs, codebooks),
+  // then the pipeline's sub-chunks (loads complete in order)
+  uint32_t qraw[2][QE];
+  float sgn[QE];
+  {
+    const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
+    const void* qsrc = dense ? static_cast<const void*>(p.qrot) : p.q;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = wave + NW * h;
+      const bool ok = rs.valid(r);
+      const int64_t qb = !ok ? 0
+                         : dense ? rs.qoff(r) * D
+                                 : b * p.q_sb + static_cast<int64_t>(rs.head(r)) * p.q_sh +
+                                       static_cast<int64_t>(rs.lpos(r)) * p.q_sl;
+#pragma unroll
+      for (int e = 0; e < QE; ++e) {
+        const int64_t i = qb + lane + e * kWave;
+        qraw[h][e] = !ok ? 0u : q32 ? static_cast<const uint32_t*>(qsrc)[i] : static_cast<const uint16_t*>(qsrc)[i];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < QE; ++e) sgn[e] = dense ? 1.f : p.krot[lane + e * kWave];
+  }
+  float ckb[1 << KB], cvb[1 << VB];
+#pragma unroll
+  for (int i = 0; i < (1 << KB); ++i) ckb[i] = p.kcb[i];
+#pragma unroll
+  for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
+  Buf buf[P];
+#pragma unroll
+  for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
+
+  // ---- pair tables (as in the small kernel): keys as hi and lo tables of
+  // 4-byte entries, values as (hi pair, lo pair) entries; values from the
+  // scalar codebook copies, since vector loads here would wait for the
+  // prefetch above
+  float kmax = 0.f, vmax = 0.f;
+#pragma unroll
+  for (int i = 0; i < (1 << KB); ++i) kmax = fmaxf(kmax, fabsf(ckb[i]));
+#pragma unroll
+  for (int i = 0; i < (1 << VB); ++i) vmax = fmaxf(vmax, fabsf(cvb[i]));
+  const float sk = f16_split_scale(kmax);
+  const float cbs_v = f16_split_scale(vmax);
+  static_assert(S::KKEYS * S::REPK / 8 <= NT && S::VKEYS * S::REPV / 8 <= NT, "one table slot per thread");
+  {
+    const int kslot = tid < S::KKEYS * S::REPK / 8 ? tid : 0;
+    const int vslot = tid < S::VKEYS * S::REPV / 8 ? tid : 0;
+    const int kkey = kslot / (S::REPK / 8), vkey = vslot / (S::REPV / 8);
+    const float cka = mux_pick<KB>(ckb, kkey & ((1 << KB) - 1)), ckb2 = mux_pick<KB>(ckb, kkey >> KB);
+    const float cva = mux_pick<VB>(cvb, vkey & ((1 << VB) - 1)), cvb2 = mux_pick<VB>(cvb, vkey >> VB);
+    if (tid < S::KKEYS * S::REPK / 8) {
+      uint32_t h0, l0, h1, l1;
+      split_f16(cka * sk, h0, l0);
+      split_f16(ckb2 * sk, h1, l1);
+      const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+      uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + kslot * 2;
+      uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + kslot * 2;
+      dh[0] = dh[1] = make_uint4(hi, hi, hi, hi);
+      dl[0] = dl[1] = make_uint4(lo, lo, lo, lo);
+    }
+    if (tid < S::VKEYS * S::REPV / 8) {
+      uint32_t h0, l0, h1, l1;
+      split_f16(cva * cbs_v, h0, l0);
+      split_f16(cvb2 * cbs_v, h1, l1);
+      const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+      uint4* d = reinterpret_cast<uint4*>(lds + S::LUTV_OFF) + vslot * 4;
+      d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
+    }
+  }
+
+  // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
+  // (dense: rotated by qprep_kernel), into LDS with each row's max |y|
+  {
+    const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = wave + NW * h;
+      float y[QE];
+#pragma unroll
+      for (int e = 0; e < QE; ++e) {
+        const uint32_t raw = qraw[h][e];
+        const float qv = q32 ? __builtin_bit_cast(float, raw)
+                             : (p.q_dtype == TQ_DTYPE_F16 ? f16_bits_to_f32(static_cast<uint16_t>(raw))
+                                                          : bf16_bits_to_f32(static_cast<uint16_t>(raw)));
+        y[e] = dense ? qv : round_q(p.q_dtype, qv * p.scale_q) * sgn[e];
+      }
+      if (!dense) {
+        wave_fwht<D>(y, lsg);
+#pragma unroll
+        for (int e = 0; e < QE; ++e) y[e] *= p.rscale;
+      }
+      float m = 0.f;
+      float* qy = reinterpret_cast<float*>(lds + S::QY_OFF) + r * D;
+#pragma unroll
+      for (int e = 0; e < QE; ++e) {
+        qy[lane + e * kWave] = y[e];
+        m = fmaxf(m, fabsf(y[e]));
+      }
+      m = wave_max(m);
+      if (lane == 0) reinterpret_cast<float*>(lds + S::QMAX_OFF)[r] = m;
+    }
+  }
+  lds_barrier();
+  // query pieces in B-operand order: staging [piece][r][g][j] holds
+  // q_r[g D/4 + 8 j + e], e = 0..7, as f16 (one hi/lo scale for all rows)
+  float qm = 0.f;
+#pragma unroll
+  for (int r = 0; r < NQ; ++r) qm = fmaxf(qm, reinterpret_cast<const float*>(lds + S::QMAX_OFF)[r]);
+  const float sq = f16_split_scale(qm);
+  for (int idx = tid; idx < NQ * D; idx += NT) {
+    const int r = idx / D;
+    const int c = idx % D;
+    uint32_t hi, lo;
+    split_f16(reinterpret_cast<const float*>(lds + S::QY_OFF)[idx] * sq, hi, lo);
+    const int qg = c / S::QTR;
+    const int j = (c % S::QTR) / 8;
+    const int e = c % 8;
+    uint16_t* st = reinterpret_cast<uint16_t*>(lds + S::QST_OFF);
+    st[(((0 * NQ + r) * 4 + qg) * NKJ + j) * 8 + e] = static_cast<uint16_t>(hi);
+    st[(((1 * NQ + r) * 4 + qg) * NKJ + j) * 8 + e] = static_cast<uint16_t>(lo);
+  }
+  lds_barrier();
+  u32x4_t qbh[NKJ], qbl[NKJ];
+#pragma unroll
+  for (int j = 0; j < NKJ; ++j) {
+    qbh[j] = lds_at<u32x4_t>(lds, S::QST_OFF + (((0 * NQ + n) * 4 + g) * NKJ + j) * 16);
+    qbl[j] = lds_at<u32x4_t>(lds, S::QST_OFF + (((1 * NQ + n) * 4 + g) * NKJ + j) * 16);
+  }
+  // score scale: S * ||k|| * log2(e) / (s_K s_Q) in log2 units
+  const float kscale = 1.4426950408889634f * __builtin_amdgcn_rcpf(sk) * __builtin_amdgcn_rcpf(sq);  // powers of two: exact
+  // causal limit of this lane's row n (keys t <= lim are visible)
+  int lim = INT32_MAX, lim_min = INT32_MAX;
+  if (p.causal) {
+    const int base_lim = static_cast<int>(Tb - p.L);
+    for (int r = 0; r < NQ; ++r)
+      if (rs.valid(r)) {
+        const int lr_ = base_lim + rs.lpos(r);
+        lim_min = min(lim_min, lr_);
+        if (n == r) lim = lr_;
+      }
+  }
+
+  // ------------------------------------------------------------ streaming ----
+  constexpr float kLazy = 7.f;
+  f32x4_t O[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) O[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_row = -INFINITY;  // reference max of row n (log2 units)
+  int E = -1000;            // value-norm exponent of the wave (max ||v|| <= 2^E when set)
+  float vsc = 0.f;          // 2^-E
+  float nv_lim = 0.f;       // 2^(E + 8): larger norms could overflow an f16 weight
+  float l_acc = 0.f;        // sum of p over this lane's tokens of row n
+
+  struct Scores {
+    f32x4_t c[2];
+  };
+  // per tile two accumulator chains (key hi parts against both query
+  // pieces, key lo parts against the query hi part)
+  auto scores = [&](const Buf& bf) -> Scores {
+    f32x4_t Ch[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    f32x4_t Cl[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int j = 0; j < NKJ; ++j)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        u32x4_t ah, al;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t a = key_addr<2 * KB, S::LOGSK>(bf.k[t], (8 * j + 2 * u) * KB, lutk_lane, kmask);
+          ah[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + a);
+          al[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
+        }
+        Ch[t] = mfma_f16(ah, qbh[j], Ch[t]);
+        Cl[t] = mfma_f16(al, qbh[j], Cl[t]);
+        Ch[t] = mfma_f16(ah, qbl[j], Ch[t]);
+      }
+    return Scores{{Ch[0] + Cl[0], Ch[1] + Cl[1]}};
+  };
+
+  auto finish = [&](const Buf& bf, const Scores& C, int s0) {
+    // ---- value operands first (independent of the softmax)
+    constexpr uint32_t MEVEN = [] {
+      uint32_t m = 0;
+      for (int j = 0; j < CPL; j += 2) m |= ((1u << VB) - 1u) << (j * VB);
+      return m;
+    }();
+    uint32_t zl[4], zh[4];
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      uint32_t xa, xb;
+      if constexpr (VRAW == 2) {
+        xa = __builtin_amdgcn_alignbit(bf.v[2 * e2][1], bf.v[2 * e2][0], vsh);
+        xb = __builtin_amdgcn_alignbit(bf.v[2 * e2 + 1][1], bf.v[2 * e2 + 1][0], vsh);
+      } else if constexpr (S::SEGBITS < 32) {
+        xa = bf.v[2 * e2][0] >> vsh;
+        xb = bf.v[2 * e2 + 1][0] >> vsh;
+      } else {
+        xa = bf.v[2 * e2][0];
+        xb = bf.v[2 * e2 + 1][0];
+      }
+      zl[e2] = (xa & MEVEN) | ((xb << VB) & ~MEVEN);
+      zh[e2] = ((xa >> VB) & MEVEN) | (xb & ~MEVEN);
+    }
+    uint2 vop[CPL][4];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const uint32_t z[1] = {(c & 1) ? zh[e2] : zl[e2]};
+        vop[c][e2] = lds_at<uint2>(lds, S::LUTV_OFF + key_addr<2 * VB, S::LOGSV>(z, (c >> 1) * 2 * VB, lutv_lane, vmask));
+      }
+    float nk[8], nv[8], sc[8], d[8];
+    {
+      float a0[4], a1[4], c0[4], c1[4];
+      norm4(bf.nk[0], a0);
+      norm4(bf.nk[1], a1);
+      norm4(bf.nv[0], c0);
+      norm4(bf.nv[1], c1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        nk[e] = a0[e];
+        nk[4 + e] = a1[e];
+        nv[e] = c0[e];
+        nv[4 + e] = c1[e];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      sc[k] = own_reg(C.c[k >> 2][k & 3]);
+      d[k] = fmaf(sc[k], nk[k] * kscale, -m_row);
+    }
+    float dmax = d[0], nvmax = nv[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) {
+      dmax = fmaxf(dmax, d[k]);
+      nvmax = fmaxf(nvmax, nv[k]);
+    }
+    const bool edge = s0 + SUB > t_end || s0 + SUB - 1 > lim_min;  // wave-uniform
+    if (edge || __any((dmax > kLazy || nvmax > nv_lim) ? 1 : 0)) {
+      // ---- slow path: masks, new reference max / norm exponent, rescale
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        sc[k] *= nk[k] * kscale;
+        if (edge) {
+          const int t = s0 + 16 * (k >> 2) + 4 * g + (k & 3);
+          if (t > lim) sc[k] = -FLT_MAX;
+          if (t >= t_end) sc[k] = -INFINITY;
+        }
+      }
+      float rm = sc[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) rm = fmaxf(rm, sc[k]);
+      rm = fmaxf(rm, xor_lane<16>(rm));
+      {
+        const float2 h = halves(rm);
+        rm = fmaxf(h.x, h.y);  // max of row n over the sub-chunk
+      }
+      const float vm = wave_max(nvmax);
+      int ev;
+      frexpf(vm, &ev);
+      const int e2 = ev > E ? ev : E;
+      const float mn = (rm > m_row + kLazy || m_row == -INFINITY) ? fmaxf(m_row, rm) : m_row;
+      // l scales by 2^(m_old - m_new), O also by 2^(E_old - E_new); both
+      // start at zero (the first sub-chunk has m_old = -inf)
+      const float am = (m_row == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_row - mn);
+      const float ao = am * ldexpf(1.f, E - e2);
+      l_acc *= am;
+      // O register i of lane group g' is row 4 g' + i: its factor sits in lane 4 g' + i
+      float ar[NQ];
+#pragma unroll
+      for (int r = 0; r < NQ; ++r) ar[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ao), r));
+      float fr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fr[i] = g == 0 ? ar[i] : g == 1 ? ar[4 + i] : g == 2 ? ar[8 + i] : ar[12 + i];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[c][i] *= fr[i];
+      m_row = mn;
+      E = e2;
+      vsc = ldexpf(1.f, -E);
+      nv_lim = ldexpf(1.f, E + 8);
+      // masked keys (-FLT_MAX) get weight 1 when their whole row is masked
+      // (m = -FLT_MAX), else 0; keys past the end (-inf) always 0
+#pragma unroll
+      for (int k = 0; k < 8; ++k) d[k] = sc[k] - m_row;
+    }
+    float w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float pe = __builtin_amdgcn_exp2f(d[k]);
+      l_acc += pe;
+      w[k] = pe * (nv[k] * vsc);
+    }
+    // ---- weights to the A operands: tile 0's four tokens, then tile 1's;
+    // each pair twice, against the (hi pair, lo pair) k slots of the values
+    const uint32_t w01 = pack_f16x2(w[0], w[1]);
+    const uint32_t w23 = pack_f16x2(w[2], w[3]);
+    const uint32_t x01 = pack_f16x2(w[4], w[5]);
+    const uint32_t x23 = pack_f16x2(w[6], w[7]);
+    const u32x4_t A0 = {w01, w01, w23, w23};
+    const u32x4_t A1 = {x01, x01, x23, x23};
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      O[c] = mfma_f16(A0, u32x4_t{vop[c][0].x, vop[c][0].y, vop[c][1].x, vop[c][1].y}, O[c]);
+      O[c] = mfma_f16(A1, u32x4_t{vop[c][2].x, vop[c][2].y, vop[c][3].x, vop[c][3].y}, O[c]);
+    }
+  };
+
+  // Loads are issued unconditionally (past t_end they read zeros for free),
+  // so the count of outstanding loads is exact for every sub-chunk.
+  Scores Cn;
+  if (n_my > 0) Cn = scores(buf[0]);
+  for (int base = 0; base < n_my; base += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const int i = base + s;
+      if (i < n_my) {
+        const Scores C = Cn;
+        finish(buf[s], C, sub_start(i));
+        if (i + 1 < n_my) Cn = scores(buf[(s + 1) % P]);
+      }
+      load_sub(buf[s], sub_start(i + P));
+    }
+  }
+
+  // --------------------------------------------------- combine the waves ----
+  // l of row n: lanes (g', n) for every g'
+  float lr = l_acc + xor_lane<16>(l_acc);
+  {
+    const float2 h = halves(lr);
+    lr = h.x + h.y;
+  }
+  lds_barrier();  // every wave is done with the tables and staging
+  float* s_wo = reinterpret_cast<float*>(lds + S::WO_OFF);
+  float* s_wm = reinterpret_cast<float*>(lds + S::WM_OFF);
+  float* s_wl = reinterpret_cast<float*>(lds + S::WL_OFF);
+  float* s_we = reinterpret_cast<float*>(lds + S::WE_OFF);
+  float* s_wf = reinterpret_cast<float*>(lds + S::WF_OFF);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float* dst = s_wo + (wave * NQ + 4 * g + i) * D + CPL * n;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) dst[c] = O[c][i];
+  }
+  if (g == 0) {
+    // a wave without tokens keeps m = -inf and contributes nothing
+    s_wm[wave * NQ + n] = m_row;
+    s_wl[wave * NQ + n] = lr;
+    s_we[wave * NQ + n] = ldexpf(1.f, E);  // undoes the weights' 2^-E
+  }
+  lds_barrier();
+  float* s_fo = reinterpret_cast<float*>(lds + S::FO_OFF);
+  float* s_fl = reinterpret_cast<float*>(lds + S::FL_OFF);
+  if (tid < NQ) {  // per row: the waves' log-sum-exp factors, l and the reference m
+    const int r = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w * NQ + r]);
+    float lt = 0.f;
+    const float oscale = __builtin_amdgcn_rcpf(cbs_v);  // a power of two: exact
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wm = s_wm[w * NQ + r];
+      const float f = wm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm - M);
+      lt = fmaf(s_wl[w * NQ + r], f, lt);
+      s_wf[w * NQ + r] = f * s_we[w * NQ + r] * oscale;
+    }
+    s_fl[r] = lt;
+    s_fl[NQ + r] = M;
+  }
+  lds_barrier();
+  for (int idx = tid; idx < NQ * D; idx += NT) {
+    const int r = idx / D;
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) a = fmaf(s_wo[(w * NQ) * D + idx], s_wf[w * NQ + r], a);
+    s_fo[idx] = a;
+  }
+  lds_barrier();
+
+  if (nvalid > 1) {
+    // this split's partial for attn_merge_kernel: o through R_V^-1 (Hadamard),
+    // then o[r][:] and (m, l) per row with m in natural-log units
+    if (!dense) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = wave + NW * h;
+        float y[QE];
+#pragma unroll
+        for (int e = 0; e < QE; ++e) y[e] = s_fo[r * D + lane + e * kWave];
+        wave_fwht<D>(y, lsg);
+#pragma unroll
+        for (int e = 0; e < QE; ++e) s_fo[r * D + lane + e * kWave] = y[e] * p.rscale * p.vrot[lane + e * kWave];
+      }
+    }
+    lds_barrier();
+    const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;
+    float4* po4 = reinterpret_cast<float4*>(p.po + (grp * p.n_splits + split) * static_cast<int64_t>(NQ) * D);
+    for (int idx = tid; idx < NQ * D / 4; idx += NT) po4[idx] = reinterpret_cast<const float4*>(s_fo)[idx];
+    if (tid < NQ) {
+      float* pm = p.pml + ((grp * p.n_splits + split) * NQ + tid) * 2;
+      pm[0] = s_fl[NQ + tid] * 0.6931471805599453f;
+      pm[1] = s_fl[tid];
+    }
+    return;
+  }
+
+  // ---- finish: o / l (0 when no token is visible), R_V^-1, store
+  if (!dense) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = wave + NW * h;
+      if (!rs.valid(r)) continue;  // wave-uniform
+      const float lt = s_fl[r];
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      float y[QE];
+#pragma unroll
+      for (int e = 0; e < QE; ++e) y[e] = s_fo[r * D + lane + e * kWave] * inv;
+      wave_fwht<D>(y, lsg);
+      const int64_t qo = rs.qoff(r) * D;
+#pragma unroll
+      for (int e = 0; e < QE; ++e)
+        store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * p.vrot[lane + e * kWave]);
+    }
+  } else {
+    for (int idx = tid; idx < NQ * D; idx += NT) {
+      const int r = idx / D;
+      const int c = idx % D;
+      if (!rs.valid(r)) continue;
+      const float lt = s_fl[r];
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      float a2 = 0.f;  // x_c = sum_k y_k R[k][c]
+      for (int k2 = 0; k2 < D; ++k2) a2 = fmaf(s_fo[r * D + k2], p.vrot[static_cast<int64_t>(k2) * D + c], a2);
+      store_out(p.out, p.q_dtype, rs.qoff(r) * D + c, a2 * inv);
+    }
+  }
+}
+
+template <int KB, int VB>
+int launch_rows16(const AttnParams& p, hipStream_t st) {
+  if (p.nq != Rows16Shape<KB, VB>::NQ)
+    return fail(TQ_ERR_UNSUPPORTED, "attention: 16-row kernel launched with %d-row groups", p.nq);
+  const dim3 grid(p.n_splits, p.Hkv * p.n_rg, p.B);
+  hipLaunchKernelGGL((attn_rows16_kernel<KB, VB>), grid, dim3(Rows16Shape<KB, VB>::NT), 0, st, p);
+  return check_launch("attn_rows16_kernel");
+}
+
+}  // namespace tq

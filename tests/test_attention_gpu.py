@@ -185,6 +185,33 @@ def test_split_with_fully_masked_rows(device, d):
     run_case(device, 80 + d, 1, 2, 2, 4, 9 * 256 + 2, d, 3, 3, causal=True)
 
 
+@pytest.mark.parametrize("Hq,Hkv,L,kb,vb,lengths", [
+    (32, 8, 4, 2, 1, None),            # config-4 shape: 16 rows (GQA 4 x 4 drafts), causal
+    (16, 8, 3, 3, 3, None),            # 6 rows: the idle columns of the group
+    (32, 2, 1, 4, 4, None),            # GQA-16 decode
+    (8, 1, 2, 1, 3, None),             # 8 heads x 2 drafts
+    (32, 8, 4, 3, 2, [5000, 3, 777]),  # ragged, one sequence shorter than the drafts
+    (4, 1, 40, 3, 3, None),            # 160 rows: ten row groups (a prefill chunk)
+    (24, 8, 4, 2, 2, [1, 4100]),       # 12 rows, ragged with a one-token sequence
+])
+def test_rows16_groups(device, Hq, Hkv, L, kb, vb, lengths):
+    """16-row groups at d = 128 (verify, wide GQA, prefill chunks)."""
+    B = 1 if lengths is None else len(lengths)
+    T = 5000 if lengths is None else max(lengths)
+    run_case(device, 300 + Hq + L + kb, B, Hq, Hkv, L, T, 128, kb, vb, lengths=lengths)
+
+
+@pytest.mark.parametrize("qdt", ["f32", "f16"])
+def test_rows16_query_dtypes_and_f16_norms(device, qdt):
+    run_case(device, 6, 2, 32, 8, 2, 1300, 128, 3, 3, qdt=qdt, norm="float16")
+
+
+def test_rows16_split_with_fully_masked_rows(device):
+    """16 causal drafts over T = 9 * 256 + 2: in the last split most rows see
+    no key, so their partials carry only masked scores."""
+    run_case(device, 81, 1, 1, 1, 16, 9 * 256 + 2, 128, 3, 3, causal=True)
+
+
 def test_empty_cache_gives_zeros(device):
     q = torch.randn(1, 8, 1, 128, dtype=torch.bfloat16, device=device)
     kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)
