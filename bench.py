@@ -45,6 +45,9 @@ CFG2 = dict(B=32, Hq=16, Hkv=8, D=256, kb=4, vb=2, lo=2048, hi=8192, seed=1004)
 CFG3 = dict(layers=36, plain_layers=4, Hkv=8, T=8192, D=128, bits=3)
 # config 4: speculative verify, 4 drafts per sequence, 131072 + 4 cached tokens, K2/V1
 CFG4 = dict(B=4, Hq=32, Hkv=8, L=4, T=131072 + 4, D=128, kb=2, vb=1)
+# prefill attention: one prefill_step_size chunk (256 queries) at the end of an
+# 8192-token prompt, config-1 heads and widths, causal
+CFGP = dict(B=1, Hq=32, Hkv=8, L=256, T=8192, D=128, bits=3)
 
 
 def algorithmic_decode_bytes(Hkv, T, D, kb, vb, norm_bytes, B=1):
@@ -151,11 +154,10 @@ def bench_quantize(torch, args, dev):
               torch.empty((B, H, T), dtype=torch.float32, device=dev)) for _ in range(2)]
             for _ in range(n_sets)]
 
-    def step(i):
+    def step(i):  # the append of update_and_fetch: keys and values in one launch
         k, v = xs[i % n_sets]
         (kp, kn), (vp, vn) = outs[i % n_sets]
-        ops.append_quantize(k, kc, kp, kn, 0)
-        ops.append_quantize(v, vc, vp, vn, 0)
+        ops.append_quantize_kv(k, v, kc, vc, kp, kn, vp, vn, 0)
 
     ms, _, _ = graph_timed(torch, step, args.steps, args.warmup, dev)
     return dict(bytes=per_call, ms_per_step=ms, kernel_bytes=per_call / 2)
@@ -257,8 +259,7 @@ def bench_prefill_append(torch, args, dev):
             ops.append_plain(v, dst[li][1], 0)
         else:
             (kp, kn), (vp, vn) = dst[li]
-            ops.append_quantize(k, kc, kp, kn, 0)
-            ops.append_quantize(v, vc, vp, vn, 0)
+            ops.append_quantize_kv(k, v, kc, vc, kp, kn, vp, vn, 0)
 
     def step(_i):
         for li in range(c["layers"]):
@@ -355,6 +356,46 @@ def bench_verify(torch, args, dev):
                            "steps": steps_p}}
 
 
+def bench_prefill_attention(torch, args, dev):
+    """A 256-query causal prefill chunk over the packed cache (32 q / 8 kv heads, d=128, 3-bit).
+
+    Roofline: matrix cores.  Algorithmic flops count the visible (causal)
+    query-key pairs once for the scores and once for the value sum, 2 flops
+    each per coordinate; the kernels run three f16 products per score
+    (hi/lo split), which the figure does not credit.
+    """
+    from kaplumba_amd import ops
+
+    c = CFGP
+    B, Hq, H, L, T, D = c["B"], c["Hq"], c["Hkv"], c["L"], c["T"], c["D"]
+    layers, kc, vc = make_layer_caches(torch, 4, c, dev)
+    g = torch.Generator(device=dev).manual_seed(5000)
+    qs = [torch.randn(B, Hq, L, D, device=dev, generator=g).to(torch.bfloat16) for _ in layers]
+    scale = 1.0 / math.sqrt(D)
+
+    def step(i):
+        (kn, kp), (vn, vp) = layers[i % len(layers)]
+        return ops.attention_packed(qs[i % len(qs)], kn, kp, vn, vp, kc, vc, scale, True)
+
+    steps = max(5, args.steps // 10)
+    ms, outs, _ = graph_timed(torch, step, steps, 3, dev)
+    if not torch.equal(outs[0], step(0)):
+        raise RuntimeError("prefill attention: graph replay differs from the eager call")
+    del layers, outs
+    _free(torch)
+    visible = sum(T - L + i + 1 for i in range(L))  # keys seen by each query position
+    flops = 4.0 * B * Hq * D * visible
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "prefill attention: one 256-query causal chunk ending an 8192-token "
+                        "prompt, 32 q / 8 kv heads, d=128, 3-bit K/V, Hadamard rotation, f32 norms",
+            "value": round(tflops, 2), "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "roofline": "mfma (f16/bf16 dense peak 2500 TFLOP/s)",
+            "us_per_step": round(ms * 1e3, 3), "flops_per_step": flops,
+            "cache_bytes": algorithmic_decode_bytes(H, T, D, c["bits"], c["bits"], 4, B),
+            "prefill_tokens_per_s": round(L * 1e3 / ms, 1), "steps": steps}
+
+
 def cpu_baseline(seconds_budget=12.0):
     """Numpy restatement of the reference's array-path attention (oracle), cfg1 shape."""
     import numpy as np
@@ -399,9 +440,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=CFG1["T"],
                     help="cached tokens per kv head of the headline decode leg (context-length "
                          "sweeps; the config-1 figure is quoted at the default 32768)")
-    ap.add_argument("--legs", default="cfg0,cfg2,cfg3,cfg4",
+    ap.add_argument("--legs", default="cfg0,cfg2,cfg3,cfg4,prefill",
                     help="comma-separated extra legs to run after the cfg1 headline "
-                         "(cfg0, cfg2, cfg3, cfg4; empty for the headline only)")
+                         "(cfg0, cfg2, cfg3, cfg4, prefill; empty for the headline only)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -415,7 +456,7 @@ def main():
     dec = bench_decode(torch, args, dev)
     _free(torch)
     legs = {x.strip() for x in args.legs.split(",") if x.strip()}
-    unknown = legs - {"cfg0", "cfg2", "cfg3", "cfg4"}
+    unknown = legs - {"cfg0", "cfg2", "cfg3", "cfg4", "prefill"}
     if unknown:
         ap.error(f"unknown legs: {sorted(unknown)}")
     value = dec["bytes"] / (dec["ms_per_step"] * 1e-3) / 1e9
@@ -449,7 +490,8 @@ def main():
     if "cfg0" in legs:
         qnt = bench_quantize(torch, args, dev)
         _free(torch)
-        line["quantize"] = {"workload": "cfg0 append-quantize K+V f16 [1,8,4096,128] 3-bit, "
+        line["quantize"] = {"workload": "cfg0 append-quantize K+V f16 [1,8,4096,128] 3-bit (one "
+                                        "tq_append_quantize_kv call, as update_and_fetch makes), "
                                         "Hadamard rotation",
                             "value": round(qnt["bytes"] / (qnt["ms_per_step"] * 1e-3) / 1e9, 2),
                             "unit": "GB/s", "step_us": round(qnt["ms_per_step"] * 1e3, 3)}
@@ -459,6 +501,8 @@ def main():
         line["cfg3"] = bench_prefill_append(torch, args, dev)
     if "cfg4" in legs:
         line["cfg4"] = bench_verify(torch, args, dev)
+    if "prefill" in legs:
+        line["prefill_attention"] = bench_prefill_attention(torch, args, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

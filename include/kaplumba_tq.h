@@ -77,6 +77,26 @@ int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
                        int64_t capacity, int64_t offset, void* stream);
 
 /*
+ * The keys and the values of one update_and_fetch (tq.py:5026-5064: its two
+ * _TurboQuantMSECodec.quantize calls, tq.py:4186-4254, and their
+ * _write_state) in one call.  Each side is exactly tq_append_quantize with
+ * its own x, strides, bits, rotation vector / matrix, midpoints and
+ * destination; the shape (B, H, L, dim), x_dtype, rot_kind, norm_dtype,
+ * capacity and offset are shared.  The Hadamard rotation with F16 / BF16
+ * input at dim 64 / 128 / 256 and equal widths or v_bits = k_bits + 1 (the
+ * x.5-bit split) runs both sides in one kernel launch; other cases run the
+ * two quantizers one after the other.  Results are identical either way.
+ */
+int tq_append_quantize_kv(const void* k_x, const void* v_x, int x_dtype, int B, int H, int L,
+                          int dim, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_l,
+                          int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_l,
+                          int k_bits, int v_bits, int rot_kind,
+                          const float* k_rot, const float* v_rot,
+                          const float* k_midpoints, const float* v_midpoints,
+                          uint32_t* k_packed, void* k_norms, uint32_t* v_packed, void* v_norms,
+                          int norm_dtype, int64_t capacity, int64_t offset, void* stream);
+
+/*
  * Append L tokens unquantized into an fp16/bf16 layer buffer (the
  * mixed-precision layers).  Replaces the slice assignment of
  * KVCache.update_and_fetch (cache.py:415-441).  dtype: F16 or BF16; x and dst

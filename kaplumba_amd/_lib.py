@@ -37,6 +37,13 @@ SIGNATURES = {
         c_int, c_int, c_void_p, c_void_p,                   # bits, rot_kind, rot, midpoints
         c_void_p, c_void_p, c_int,                          # packed, norms, norm_dtype
         c_int64, c_int64, c_void_p]),                       # capacity, offset, stream
+    "tq_append_quantize_kv": (c_int, [
+        c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,   # k_x, v_x, dtype, B, H, L, dim
+        c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,    # k strides, v strides
+        c_int, c_int, c_int, c_void_p, c_void_p,                 # k_bits, v_bits, rot_kind, rots
+        c_void_p, c_void_p,                                      # midpoints
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,           # k packed/norms, v packed/norms, norm_dtype
+        c_int64, c_int64, c_void_p]),                            # capacity, offset, stream
     "tq_append_plain": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int, c_int,
         c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),

@@ -172,8 +172,8 @@ class BatchTurboQuantKVCache(_LeftPadded, _BaseCache):
                                  f"{tuple(self.keys.norms.shape[:2])}")
             self.keys = self._grow(self.keys, new_end)
             self.values = self._grow(self.values, new_end)
-        ops.append_quantize(keys, self.key_codec, self.keys.indices, self.keys.norms, prev)
-        ops.append_quantize(values, self.value_codec, self.values.indices, self.values.norms, prev)
+        ops.append_quantize_kv(keys, values, self.key_codec, self.value_codec, self.keys.indices,
+                               self.keys.norms, self.values.indices, self.values.norms, prev)
         self.offset = self.offset + L
         self._idx = new_end
         return (_QuantizedStateProxy(self._sliced(self.keys), self._idx, H, keys.shape[-1], B),

@@ -269,9 +269,9 @@ class TurboQuantKVCache(_BaseCache):
                                  f"{tuple(self.keys.norms.shape[:2])}")
             self.keys = self._grow(self.keys, self.key_codec, new_end)
             self.values = self._grow(self.values, self.value_codec, new_end)
-        ops.append_quantize(keys, self.key_codec, self.keys.indices, self.keys.norms, self.offset)
-        ops.append_quantize(values, self.value_codec, self.values.indices, self.values.norms,
-                            self.offset)
+        ops.append_quantize_kv(keys, values, self.key_codec, self.value_codec, self.keys.indices,
+                               self.keys.norms, self.values.indices, self.values.norms,
+                               self.offset)
         self.offset = new_end
         ks, vs = self.state
         return (

@@ -55,8 +55,10 @@ __device__ __forceinline__ void load32(const void* p, float (&v)[32]) {
   }
 }
 
+// One block's share of a quantize launch: vectors [block * VPB, block * VPB + VPB)
+// of a (256 threads).  Shared by the one-tensor and the key + value kernels.
 template <int D, int BITS, int XDT>
-__global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
+__device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t block) {
   constexpr int NL = D / 32;          // lanes per vector
   constexpr int VPB = 256 / NL;       // vectors per block
   constexpr int NMID = (1 << BITS) - 1;
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
   const bool use_lut = LUT && s_qb_bad == 0;
 
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
-  const int64_t vec = static_cast<int64_t>(blockIdx.x) * VPB + threadIdx.x / NL;
+  const int64_t vec = block * VPB + threadIdx.x / NL;
   const int g = threadIdx.x % NL;
   // Every lane of a vector shares `vec`, so a vector's lanes leave together
   // and the xor-shuffles below stay inside live lane groups.
@@ -184,6 +186,23 @@ __global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
     else
       static_cast<float*>(a.norms)[row] = n;
   }
+}
+
+template <int D, int BITS, int XDT>
+__global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
+  rht_quantize_block<D, BITS, XDT>(a, blockIdx.x);
+}
+
+// Keys and values of one update_and_fetch in one launch: blocks below
+// k_blocks quantize the keys, the rest the values (each block one side, so
+// the branch is uniform).  One launch instead of two halves the fixed cost
+// (launch, first-load latency, tail) of a decode or prefill append.
+template <int D, int KBITS, int VBITS, int XDT>
+__global__ __launch_bounds__(256) void append_rht_kv_kernel(AppendArgs k, AppendArgs v, int64_t k_blocks) {
+  if (static_cast<int64_t>(blockIdx.x) < k_blocks)
+    rht_quantize_block<D, KBITS, XDT>(k, blockIdx.x);
+  else
+    rht_quantize_block<D, VBITS, XDT>(v, blockIdx.x - k_blocks);
 }
 
 // ------------------------------------------------------------------ plain ---
@@ -306,14 +325,53 @@ int launch_append_rht(int bits, int x_dtype, const AppendArgs& a, hipStream_t st
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+template <int D, int KBITS, int VBITS, int XDT>
+int launch_kv_pair(const AppendArgs& k, const AppendArgs& v, hipStream_t st) {
+  constexpr int VPB = 256 / (D / 32);
+  const int64_t n_vec = static_cast<int64_t>(k.B) * k.H * k.L;
+  const int64_t kb = (n_vec + VPB - 1) / VPB;
+  if (2 * kb > 0x7fffffff) return fail(TQ_ERR_INVALID_ARGUMENT, "append: too many vectors");
+  hipLaunchKernelGGL((append_rht_kv_kernel<D, KBITS, VBITS, XDT>), dim3(static_cast<unsigned>(2 * kb)),
+                     dim3(256), 0, st, k, v, kb);
+  return check_launch("append_rht_kv_kernel");
+}
+
+// Paired launch for equal widths or the x.5-bit split (values one bit wider),
+// 16-bit inputs and head dims 64 / 128 / 256; returns -1 for other cases
+// (the caller then launches the two sides separately).
+template <int D, int XDT>
+int launch_kv_bits(int kbits, int vbits, const AppendArgs& k, const AppendArgs& v, hipStream_t st) {
+  switch (kbits * 8 + vbits) {
+    case 1 * 8 + 1: return launch_kv_pair<D, 1, 1, XDT>(k, v, st);
+    case 2 * 8 + 2: return launch_kv_pair<D, 2, 2, XDT>(k, v, st);
+    case 3 * 8 + 3: return launch_kv_pair<D, 3, 3, XDT>(k, v, st);
+    case 4 * 8 + 4: return launch_kv_pair<D, 4, 4, XDT>(k, v, st);
+    case 1 * 8 + 2: return launch_kv_pair<D, 1, 2, XDT>(k, v, st);
+    case 2 * 8 + 3: return launch_kv_pair<D, 2, 3, XDT>(k, v, st);
+    case 3 * 8 + 4: return launch_kv_pair<D, 3, 4, XDT>(k, v, st);
+  }
+  return -1;
+}
+
+template <int D>
+int launch_kv_dtype(int x_dtype, int kbits, int vbits, const AppendArgs& k, const AppendArgs& v,
+                    hipStream_t st) {
+  if (x_dtype == TQ_DTYPE_F16) return launch_kv_bits<D, TQ_DTYPE_F16>(kbits, vbits, k, v, st);
+  if (x_dtype == TQ_DTYPE_BF16) return launch_kv_bits<D, TQ_DTYPE_BF16>(kbits, vbits, k, v, st);
+  return -1;
+}
+
 }  // namespace
 
-extern "C" int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
-                                  int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
-                                  int bits, int rot_kind, const float* rot,
-                                  const float* midpoints, uint32_t* packed, void* norms,
-                                  int norm_dtype, int64_t capacity, int64_t offset,
-                                  void* stream) {
+namespace {
+
+// Argument checks of one quantize call; fills a on success.  *empty is set
+// when there is nothing to do.
+int check_append(const void* x, int x_dtype, int B, int H, int L, int dim, int64_t sb, int64_t sh,
+                 int64_t sl, int bits, const float* rot, const float* midpoints, uint32_t* packed,
+                 void* norms, int norm_dtype, int64_t capacity, int64_t offset, AppendArgs& a,
+                 bool* empty) {
+  *empty = false;
   if (B < 0 || H < 0 || L < 0) return fail(TQ_ERR_INVALID_ARGUMENT, "append: negative shape");
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "append: bits %d not in 1..4", bits);
   if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
@@ -323,16 +381,21 @@ extern "C" int tq_append_quantize(const void* x, int x_dtype, int B, int H, int 
   if (offset < 0 || offset + L > capacity)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append: tokens [%lld, %lld) exceed capacity %lld",
                 (long long)offset, (long long)(offset + L), (long long)capacity);
-  if (static_cast<int64_t>(B) * H * L == 0) return TQ_OK;
+  if (static_cast<int64_t>(B) * H * L == 0) {
+    *empty = true;
+    return TQ_OK;
+  }
   if (!x || !rot || !midpoints || !packed || !norms)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append: null pointer");
   const int es = x_dtype == TQ_DTYPE_F32 ? 4 : 2;
-  if (!aligned16(x) || (x_stride_b * es) % 16 || (x_stride_h * es) % 16 || (x_stride_l * es) % 16)
+  if (!aligned16(x) || (sb * es) % 16 || (sh * es) % 16 || (sl * es) % 16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append: x and its strides must be 16-byte aligned");
-  AppendArgs a{x, x_stride_b, x_stride_h, x_stride_l, B, H, L, rot, midpoints, packed, norms,
-               norm_dtype, capacity, offset, 1.0f / sqrtf(static_cast<float>(dim))};
-  a.scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  a = AppendArgs{x, sb, sh, sl, B, H, L, rot, midpoints, packed, norms, norm_dtype, capacity, offset,
+                 static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)))};
+  return TQ_OK;
+}
+
+int launch_one(const AppendArgs& a, int dim, int bits, int x_dtype, int rot_kind, hipStream_t st) {
   if (rot_kind == TQ_ROT_HADAMARD) {
     switch (dim) {
       case 32: return launch_append_rht<32>(bits, x_dtype, a, st);
@@ -345,6 +408,54 @@ extern "C" int tq_append_quantize(const void* x, int x_dtype, int B, int H, int 
   }
   if (rot_kind == TQ_ROT_DENSE) return launch_append_dense(a, dim, bits, x_dtype, st);
   return fail(TQ_ERR_INVALID_ARGUMENT, "append: rot_kind %d", rot_kind);
+}
+
+}  // namespace
+
+extern "C" int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
+                                  int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
+                                  int bits, int rot_kind, const float* rot,
+                                  const float* midpoints, uint32_t* packed, void* norms,
+                                  int norm_dtype, int64_t capacity, int64_t offset,
+                                  void* stream) {
+  AppendArgs a{};
+  bool empty = false;
+  int rc = check_append(x, x_dtype, B, H, L, dim, x_stride_b, x_stride_h, x_stride_l, bits, rot,
+                        midpoints, packed, norms, norm_dtype, capacity, offset, a, &empty);
+  if (rc || empty) return rc;
+  return launch_one(a, dim, bits, x_dtype, rot_kind, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tq_append_quantize_kv(const void* k_x, const void* v_x, int x_dtype, int B, int H,
+                                     int L, int dim, int64_t k_stride_b, int64_t k_stride_h,
+                                     int64_t k_stride_l, int64_t v_stride_b, int64_t v_stride_h,
+                                     int64_t v_stride_l, int k_bits, int v_bits, int rot_kind,
+                                     const float* k_rot, const float* v_rot,
+                                     const float* k_midpoints, const float* v_midpoints,
+                                     uint32_t* k_packed, void* k_norms, uint32_t* v_packed,
+                                     void* v_norms, int norm_dtype, int64_t capacity,
+                                     int64_t offset, void* stream) {
+  AppendArgs ka{}, va{};
+  bool empty = false;
+  int rc = check_append(k_x, x_dtype, B, H, L, dim, k_stride_b, k_stride_h, k_stride_l, k_bits, k_rot,
+                        k_midpoints, k_packed, k_norms, norm_dtype, capacity, offset, ka, &empty);
+  if (rc) return rc;
+  rc = check_append(v_x, x_dtype, B, H, L, dim, v_stride_b, v_stride_h, v_stride_l, v_bits, v_rot,
+                    v_midpoints, v_packed, v_norms, norm_dtype, capacity, offset, va, &empty);
+  if (rc || empty) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rot_kind == TQ_ROT_HADAMARD) {
+    switch (dim) {
+      case 64: rc = launch_kv_dtype<64>(x_dtype, k_bits, v_bits, ka, va, st); break;
+      case 128: rc = launch_kv_dtype<128>(x_dtype, k_bits, v_bits, ka, va, st); break;
+      case 256: rc = launch_kv_dtype<256>(x_dtype, k_bits, v_bits, ka, va, st); break;
+      default: rc = -1;
+    }
+    if (rc != -1) return rc;
+  }
+  rc = launch_one(ka, dim, k_bits, x_dtype, rot_kind, st);
+  if (rc) return rc;
+  return launch_one(va, dim, v_bits, x_dtype, rot_kind, st);
 }
 
 extern "C" int tq_append_plain(const void* x, int dtype, int B, int H, int L, int dim,

@@ -89,6 +89,23 @@ def append_quantize(x: torch.Tensor, codec: Codec, packed: torch.Tensor, norms: 
     packed: (B, H, cap, PW) uint32 contiguous; norms: (B, H, cap) f32/f16 contiguous.
     """
     _require_device(x, packed, norms)
+    x = _check_append_buffers(x, codec, packed, norms)
+    B, H, L, D = x.shape
+    cap = packed.shape[2]
+    dt = codec.device_tensors(x.device)
+    lib = _lib.load()
+    rc = lib.tq_append_quantize(
+        x.data_ptr(), _lib.torch_dtype_code(x.dtype), B, H, L, D,
+        x.stride(0), x.stride(1), x.stride(2),
+        codec.bits, codec.rot_kind, dt["rot"].data_ptr(), dt["midpoints"].data_ptr(),
+        packed.data_ptr(), norms.data_ptr(), _lib.torch_dtype_code(norms.dtype),
+        cap, offset, _stream(x))
+    _lib.check(rc, "tq_append_quantize")
+
+
+def _check_append_buffers(x: torch.Tensor, codec: Codec, packed: torch.Tensor,
+                          norms: torch.Tensor) -> torch.Tensor:
+    """Validated (and, if needed, compacted) input of one quantize side."""
     B, H, L, D = x.shape
     if D != codec.dim:
         raise ValueError(f"head dim {D} != codec dim {codec.dim}")
@@ -103,15 +120,37 @@ def append_quantize(x: torch.Tensor, codec: Codec, packed: torch.Tensor, norms: 
     es = x.element_size()
     if x.data_ptr() % 16 or any((s * es) % 16 for s in x.stride()[:3]):
         x = x.contiguous()
-    dt = codec.device_tensors(x.device)
-    lib = _lib.load()
-    rc = lib.tq_append_quantize(
-        x.data_ptr(), _lib.torch_dtype_code(x.dtype), B, H, L, D,
-        x.stride(0), x.stride(1), x.stride(2),
-        codec.bits, codec.rot_kind, dt["rot"].data_ptr(), dt["midpoints"].data_ptr(),
-        packed.data_ptr(), norms.data_ptr(), _lib.torch_dtype_code(norms.dtype),
-        cap, offset, _stream(x))
-    _lib.check(rc, "tq_append_quantize")
+    return x
+
+
+def append_quantize_kv(k: torch.Tensor, v: torch.Tensor, key_codec: Codec, value_codec: Codec,
+                       k_packed: torch.Tensor, k_norms: torch.Tensor, v_packed: torch.Tensor,
+                       v_norms: torch.Tensor, offset: int) -> None:
+    """Quantize keys and values (B, H, L, D) of one append in one library call.
+
+    Both sides share shape, dtype, rotation kind, norm dtype and capacity;
+    anything else goes through two append_quantize calls.
+    """
+    same = (k.shape == v.shape and k.dtype == v.dtype and key_codec.dim == value_codec.dim
+            and key_codec.rot_kind == value_codec.rot_kind and k_norms.dtype == v_norms.dtype
+            and k_packed.shape[2] == v_packed.shape[2])
+    if not same:
+        append_quantize(k, key_codec, k_packed, k_norms, offset)
+        append_quantize(v, value_codec, v_packed, v_norms, offset)
+        return
+    _require_device(k, v, k_packed, k_norms, v_packed, v_norms)
+    k = _check_append_buffers(k, key_codec, k_packed, k_norms)
+    v = _check_append_buffers(v, value_codec, v_packed, v_norms)
+    B, H, L, D = k.shape
+    kt, vt = key_codec.device_tensors(k.device), value_codec.device_tensors(k.device)
+    rc = _lib.load().tq_append_quantize_kv(
+        k.data_ptr(), v.data_ptr(), _lib.torch_dtype_code(k.dtype), B, H, L, D,
+        k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
+        key_codec.bits, value_codec.bits, key_codec.rot_kind, kt["rot"].data_ptr(),
+        vt["rot"].data_ptr(), kt["midpoints"].data_ptr(), vt["midpoints"].data_ptr(),
+        k_packed.data_ptr(), k_norms.data_ptr(), v_packed.data_ptr(), v_norms.data_ptr(),
+        _lib.torch_dtype_code(k_norms.dtype), k_packed.shape[2], offset, _stream(k))
+    _lib.check(rc, "tq_append_quantize_kv")
 
 
 def append_plain(x: torch.Tensor, dst: torch.Tensor, offset: int) -> None:

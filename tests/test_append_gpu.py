@@ -148,3 +148,54 @@ def test_plain_append_copies_rows(device):
     ops.append_plain(x.transpose(1, 2).contiguous().transpose(1, 2), dst, 7)
     assert torch.equal(dst[:, :, 7:12], x)
     assert not dst[:, :, :7].any() and not dst[:, :, 12:].any()
+
+
+@pytest.mark.parametrize("d,kb,vb,dtype", [
+    (128, 3, 3, torch.float16),    # config 0: one paired launch
+    (64, 1, 2, torch.bfloat16),    # x.5-bit split (values one bit wider), paired
+    (256, 4, 4, torch.float16),
+    (128, 2, 3, torch.bfloat16),
+    (128, 4, 3, torch.float16),    # keys wider: two launches
+    (128, 3, 3, torch.float32),    # f32 input: two launches
+    (512, 2, 2, torch.float16),    # dim outside the paired set: two launches
+])
+@pytest.mark.parametrize("norm_dtype", [torch.float32, torch.float16])
+def test_key_value_pair_append(device, d, kb, vb, dtype, norm_dtype):
+    """tq_append_quantize_kv: both sides bit-exact against the oracle, strided
+    inputs, an offset inside the capacity, untouched rows around it."""
+    rng = np.random.default_rng(d + 10 * kb + vb)
+    B, H, L = 2, 4, 29
+    k32, _ = _synth(rng, (B, H, L, d), dtype)
+    v32, _ = _synth(rng, (B, H, L, d), dtype)
+    ks = torch.from_numpy(k32).to(dtype).transpose(1, 2).contiguous().transpose(1, 2).to(device)
+    vs = torch.from_numpy(v32).to(dtype).to(device)
+    kc, vc = ops.Codec(d, kb, 0), ops.Codec(d, vb, 1)
+    kp, kn = _buffers(B, H, 40, kc, norm_dtype, device)
+    vp, vn = _buffers(B, H, 40, vc, norm_dtype, device)
+    ops.append_quantize_kv(ks, vs, kc, vc, kp, kn, vp, vn, 5)
+    nd = "float16" if norm_dtype == torch.float16 else "float32"
+    for x, p, n, bits, seed in ((ks, kp, kn, kb, 0), (vs, vp, vn, vb, 1)):
+        wp, wn = O.quantize_rht(x.float().cpu().numpy(), bits, O.rht_signs(d, seed),
+                                O.beta_codebook(d, bits), nd)
+        gp, gn = _np_u32(p), n.float().cpu().numpy()
+        assert np.array_equal(gp[:, :, 5:5 + L], wp), (d, kb, vb, seed)
+        assert np.array_equal(gn[:, :, 5:5 + L], wn), (d, kb, vb, seed)
+        assert not gp[:, :, :5].any() and not gp[:, :, 5 + L:].any()
+        assert not gn[:, :, :5].any() and not gn[:, :, 5 + L:].any()
+
+
+def test_key_value_pair_append_dense_rotation(device):
+    """Dense rotation goes through the two matrix-core launches: identical to
+    two single-side calls."""
+    rng = np.random.default_rng(77)
+    B, H, L, d = 1, 4, 40, 128
+    k = torch.from_numpy(rng.standard_normal((B, H, L, d)).astype(np.float32)).half().to(device)
+    v = torch.from_numpy(rng.standard_normal((B, H, L, d)).astype(np.float32)).half().to(device)
+    kc, vc = ops.Codec(d, 3, 0, "dense"), ops.Codec(d, 4, 1, "dense")
+    a = [_buffers(B, H, 48, c, torch.float32, device) for c in (kc, vc)]
+    b = [_buffers(B, H, 48, c, torch.float32, device) for c in (kc, vc)]
+    ops.append_quantize_kv(k, v, kc, vc, a[0][0], a[0][1], a[1][0], a[1][1], 3)
+    ops.append_quantize(k, kc, b[0][0], b[0][1], 3)
+    ops.append_quantize(v, vc, b[1][0], b[1][1], 3)
+    for (p1, n1), (p2, n2) in zip(a, b):
+        assert torch.equal(p1, p2) and torch.equal(n1, n2)

@@ -93,3 +93,25 @@ def test_check_maps_status_to_exceptions():
         _lib.check(_lib.TQ_ERR_UNSUPPORTED, "x")
     with pytest.raises(_lib.TurboQuantLibraryError):
         _lib.check(_lib.TQ_ERR_HIP, "x")
+
+
+def test_key_value_append_checks_both_sides_without_the_gpu():
+    lib = _lib.load()
+    base = [None, None, 1, 1, 2, 1, 128, 256, 128, 128, 256, 128, 128, 3, 3, 0,
+            None, None, None, None, None, None, None, None, 0, 16, 0, None]
+    for side in (13, 14):                          # k_bits, then v_bits (L = 0: no pointer use)
+        args = list(base)
+        args[5] = 0
+        args[side] = 5
+        assert lib.tq_append_quantize_kv(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
+        assert b"bits" in lib.tq_last_error()
+    args = list(base)
+    args[25] = 0                                   # capacity 0 < offset + L
+    assert lib.tq_append_quantize_kv(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
+    assert b"capacity" in lib.tq_last_error()
+    args = list(base)
+    assert lib.tq_append_quantize_kv(*args) == _lib.TQ_ERR_INVALID_ARGUMENT  # null pointers
+    assert b"null" in lib.tq_last_error()
+    args = list(base)
+    args[5] = 0                                    # L = 0: nothing to do
+    assert lib.tq_append_quantize_kv(*args) == _lib.TQ_OK
