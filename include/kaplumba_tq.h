@@ -118,6 +118,43 @@ int tq_dequantize(const uint32_t* packed, const void* norms, int norm_dtype,
                   float* out, void* stream);
 
 /*
+ * Prod codec (_TurboQuantProdCodec, tq.py:4572-4766): MSE at mb = bits - 1
+ * bits plus a one-bit QJL sketch of the residual.  Replaces its quantize
+ * (array path, tq.py:4653-4666; the fused single-token kernel,
+ * tq.py:2968-3116, computes the same quantities): for every vector x,
+ *   n = ||x||_2 (f32), u = x / max(n, 1e-6),
+ *   idx = MSE indices of u at mb bits (Hadamard rotation with `signs`, the
+ *         midpoints and order of tq_append_quantize), packed to mse_packed
+ *         [B, H, capacity, dim*mb/32]; with bits == 1 there is no MSE part,
+ *   r = u - s * (H(codebook[idx]) / sqrt(dim))   (u when bits == 1),
+ *   rn = ||r||_2, signs of r @ P^T (1 where >= 0) packed one bit each to
+ *   qjl_signs [B, H, capacity, dim/32]; n and rn go to norms / residual_norms
+ *   [B, H, capacity] in norm_dtype.
+ * P (projection, dim x dim f32 row-major, 16-byte aligned) is
+ * default_rng(seed + 1 + 2971*dim + 17).standard_normal (tq.py:3579-3584).
+ * dim in {64, 128, 256}; the workspace (>= tq_prod_workspace_size bytes,
+ * 16-byte aligned) holds the f32 residuals between the two kernels.
+ */
+int64_t tq_prod_workspace_size(int B, int H, int L, int dim);
+int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
+                     int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
+                     int bits, const float* signs, const float* mse_midpoints,
+                     const float* mse_codebook, const float* projection,
+                     uint32_t* mse_packed, void* norms, uint32_t* qjl_signs,
+                     void* residual_norms, int norm_dtype, int64_t capacity, int64_t offset,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Prod dequantize (tq.py:4668-4677), f32 [B, H, T, dim]:
+ *   out = n * (s * H(codebook[idx]) / sqrt(dim) + sqrt(pi/2)/dim * rn * (q @ P)),
+ * q_j = +1 where sign bit j is set, else -1.
+ */
+int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed, const void* residual_norms,
+                       const uint32_t* qjl_signs, int norm_dtype, int B, int H, int T, int dim,
+                       int bits, int64_t capacity, const float* signs, const float* mse_codebook,
+                       const float* projection, float* out, void* stream);
+
+/*
  * Bytes of workspace tq_attention() needs for this problem (split-K partials,
  * rotated queries and merge counters).  max_tokens is the largest
  * per-sequence cache length.

@@ -44,6 +44,17 @@ SIGNATURES = {
         c_void_p, c_void_p,                                      # midpoints
         c_void_p, c_void_p, c_void_p, c_void_p, c_int,           # k packed/norms, v packed/norms, norm_dtype
         c_int64, c_int64, c_void_p]),                            # capacity, offset, stream
+    "tq_prod_workspace_size": (c_int64, [c_int, c_int, c_int, c_int]),
+    "tq_prod_quantize": (c_int, [
+        c_void_p, c_int, c_int, c_int, c_int, c_int,           # x, dtype, B, H, L, dim
+        c_int64, c_int64, c_int64,                              # strides
+        c_int, c_void_p, c_void_p, c_void_p, c_void_p,          # bits, signs, mids, codebook, P
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,          # mse, norms, qjl signs, rnorms, norm_dtype
+        c_int64, c_int64, c_void_p, c_int64, c_void_p]),        # capacity, offset, workspace, bytes, stream
+    "tq_prod_dequantize": (c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,          # norms, mse, rnorms, signs, norm_dtype
+        c_int, c_int, c_int, c_int, c_int, c_int64,             # B, H, T, dim, bits, capacity
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),     # signs, codebook, P, out, stream
     "tq_append_plain": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int, c_int,
         c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),

@@ -154,6 +154,14 @@ def midpoints(cb: np.ndarray) -> np.ndarray:
     return ((cb[:-1] + cb[1:]) / np.float32(2)).astype(np.float32)
 
 
+def projection_matrix(dim: int, seed: int) -> np.ndarray:
+    """Gaussian QJL projection of the Prod codec (``_projection_matrix``,
+    turboquant_cache.py:3579-3584): ``default_rng(seed + 2971 dim + 17)``
+    standard normals, f32 (dim, dim).  The codec passes ``seed + 1`` (:4577)."""
+    rng = np.random.default_rng(seed + dim * 2971 + 17)
+    return rng.standard_normal((dim, dim), dtype=np.float32)
+
+
 def packed_width(length: int, bits: int) -> int:
     """u32 words per packed row (turboquant_cache.py:3699-3702)."""
     if length == 0 or bits == 0:

@@ -20,5 +20,8 @@ struct AppendArgs {
 
 // Dense-rotation quantizer on the matrix cores (tq_append_dense.hip).
 int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
+// The same product for f32 input with a one-bit output (x @ R^T >= 0), the
+// Prod codec's QJL signs; norms receive ||x||.
+int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st);
 
 }  // namespace tq

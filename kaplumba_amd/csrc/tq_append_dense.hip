@@ -93,7 +93,9 @@ __device__ __forceinline__ float x_elem(const u32x4_t (&xr)[NX], int e) {
   }
 }
 
-template <int D, int BITS, int XDT>
+// GE: one-bit signs of x @ R^T, bit = (y >= 0) (the QJL sketch of the Prod
+// codec, turboquant_cache.py:4662-4663); midpoints are not read.
+template <int D, int BITS, int XDT, bool GE = false>
 __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs a) {
   using S = DenseShape<D>;
   using XP = XPieces<XDT>;
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
   }
   float mid[NMID];
 #pragma unroll
-  for (int m = 0; m < NMID; ++m) mid[m] = a.mid[m];
+  for (int m = 0; m < NMID; ++m) mid[m] = GE ? 0.f : a.mid[m];
   __syncthreads();
 
   for (; tile * S::VPT < n_vec; tile += tile_stride) {
@@ -247,7 +249,7 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
           const float y = acc[2 * p + e / 16][e % 16];
           uint32_t idx = 0;
 #pragma unroll
-          for (int m = 0; m < NMID; ++m) idx += (y > thr[m]) ? 1u : 0u;
+          for (int m = 0; m < NMID; ++m) idx += (GE ? (y >= thr[m]) : (y > thr[m])) ? 1u : 0u;
           const int pos = e * BITS;
           const int wi = pos >> 5;
           const int sh = pos & 31;
@@ -302,7 +304,29 @@ int launch_dense_dim(const AppendArgs& a, int bits, int x_dtype, hipStream_t st)
   return fail(TQ_ERR_INVALID_ARGUMENT, "append: bits %d not in 1..4", bits);
 }
 
+template <int D>
+int launch_dense_signs_dim(const AppendArgs& a, hipStream_t st) {
+  using S = DenseShape<D>;
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  const int64_t tiles = (n_vec + S::VPT - 1) / S::VPT;
+  const int64_t per_slice = std::min<int64_t>(tiles, std::max(1, device_cu_count() / S::NSLICE));
+  hipLaunchKernelGGL((append_dense_kernel<D, 1, TQ_DTYPE_F32, true>), dim3(static_cast<unsigned>(per_slice * S::NSLICE)),
+                     dim3(kDenseThreads), 0, st, a);
+  return check_launch("append_dense_kernel (signs)");
+}
+
 }  // namespace
+
+int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(a.rot) & 15u) != 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "prod: projection matrix must be 16-byte aligned");
+  switch (dim) {
+    case 64: return launch_dense_signs_dim<64>(a, st);
+    case 128: return launch_dense_signs_dim<128>(a, st);
+    case 256: return launch_dense_signs_dim<256>(a, st);
+  }
+  return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d not in {64, 128, 256}", dim);
+}
 
 int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st) {
   if ((reinterpret_cast<uintptr_t>(a.rot) & 15u) != 0)

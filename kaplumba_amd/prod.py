@@ -1,0 +1,130 @@
+"""Prod codec: MSE at bits - 1 plus a one-bit QJL sketch of the residual.
+
+Mirrors ``_TurboQuantProdCodec`` (turboquant_cache.py:4572-4766) over torch
+device tensors and the HIP kernels of libkaplumba_tq.so: ``quantize`` (norm,
+MSE indices, residual, signs of ``residual @ P^T``), ``dequantize`` and
+attention with Prod-coded keys (``ops.attention_prod``).  The reference
+defines the codec but never builds one (no cache constructs it); here it is
+reachable through ``ProdCodec`` and ``TurboQuantKVCache(key_quantizer="prod")``.
+
+State per token (``TurboQuantProdState``, :3453-3457): norms, MSE indices
+(bits - 1 per coordinate, none at 1 bit), residual norms, QJL sign bits.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, NamedTuple, Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from . import codebook as cbmod
+from .ops import Codec, _capacity_of, _require_device, _stream
+
+__all__ = ["ProdCodec", "TurboQuantProdState"]
+
+
+class TurboQuantProdState(NamedTuple):
+    """(norms, mse_indices, residual_norms, qjl_signs) -- turboquant_cache.py:3453-3457."""
+
+    norms: torch.Tensor
+    mse_indices: torch.Tensor
+    residual_norms: torch.Tensor
+    qjl_signs: torch.Tensor
+
+
+class ProdCodec:
+    """``_TurboQuantProdCodec(dim, bits, seed)``: the MSE codec at ``bits - 1``
+    with ``seed`` (Hadamard rotation: power-of-two dims only), the projection
+    drawn with ``seed + 1`` and ``scale = sqrt(pi / 2) / dim`` (:4573-4585)."""
+
+    def __init__(self, dim: int, bits: int, seed: int):
+        if dim not in (64, 128, 256):
+            raise NotImplementedError(f"Prod codec kernels are built for head dims 64/128/256, got {dim}")
+        if int(bits) != bits or not 1 <= bits <= 4:
+            raise ValueError(f"Prod codec bits must be 1..4, got {bits}")
+        self.dim = dim
+        self.bits = int(bits)
+        self.seed = seed
+        self.mse_bits = self.bits - 1
+        # the rotation signs come from the MSE codec's seed even at 0 MSE bits
+        self.mse_codec = Codec(dim, max(self.mse_bits, 1), seed, "hadamard")
+        self.projection = cbmod.projection_matrix(dim, seed + 1)
+        self.scale = math.sqrt(math.pi / 2) / dim
+        self.mse_width = cbmod.packed_width(dim, self.mse_bits)
+        self.sign_width = dim // 32
+        self._dev: Dict[str, Dict[str, torch.Tensor]] = {}
+
+    def device_tensors(self, device) -> Dict[str, torch.Tensor]:
+        key = str(device)
+        d = self._dev.get(key)
+        if d is None:
+            m = self.mse_codec.device_tensors(device)
+            d = {"signs": m["rot"], "codebook": m["codebook"], "midpoints": m["midpoints"],
+                 "projection": torch.from_numpy(np.ascontiguousarray(self.projection)).to(device)}
+            self._dev[key] = d
+        return d
+
+    def alloc(self, B: int, H: int, cap: int, device, norm_dtype=torch.float32) -> TurboQuantProdState:
+        return TurboQuantProdState(
+            torch.zeros((B, H, cap), dtype=norm_dtype, device=device),
+            torch.zeros((B, H, cap, self.mse_width), dtype=torch.uint32, device=device),
+            torch.zeros((B, H, cap), dtype=norm_dtype, device=device),
+            torch.zeros((B, H, cap, self.sign_width), dtype=torch.uint32, device=device))
+
+    def quantize_into(self, x: torch.Tensor, st: TurboQuantProdState, offset: int) -> None:
+        """Quantize x (B, H, L, D) into rows offset .. offset + L of capacity buffers."""
+        _require_device(x, *st)
+        B, H, L, D = x.shape
+        if D != self.dim:
+            raise ValueError(f"head dim {D} != codec dim {self.dim}")
+        cap = st.norms.shape[2]
+        want = ((B, H, cap), (B, H, cap, self.mse_width), (B, H, cap), (B, H, cap, self.sign_width))
+        if tuple(tuple(t.shape) for t in st) != want or not all(t.is_contiguous() for t in st):
+            raise ValueError(f"Prod state buffers must be contiguous {want}")
+        if st.norms.dtype != st.residual_norms.dtype:
+            raise ValueError("norms and residual norms must share a dtype")
+        es = x.element_size()
+        if x.stride(-1) != 1 or x.data_ptr() % 16 or any((s * es) % 16 for s in x.stride()[:3]):
+            x = x.contiguous()
+        lib = _lib.load()
+        wsb = lib.tq_prod_workspace_size(B, H, L, D)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=x.device)
+        dt = self.device_tensors(x.device)
+        mse = st.mse_indices.data_ptr() if self.mse_bits > 0 else None
+        rc = lib.tq_prod_quantize(
+            x.data_ptr(), _lib.torch_dtype_code(x.dtype), B, H, L, D,
+            x.stride(0), x.stride(1), x.stride(2), self.bits, dt["signs"].data_ptr(),
+            dt["midpoints"].data_ptr(), dt["codebook"].data_ptr(), dt["projection"].data_ptr(),
+            mse, st.norms.data_ptr(), st.qjl_signs.data_ptr(), st.residual_norms.data_ptr(),
+            _lib.torch_dtype_code(st.norms.dtype), cap, offset, ws.data_ptr(), ws.numel(),
+            _stream(x))
+        _lib.check(rc, "tq_prod_quantize")
+
+    def quantize(self, vectors: torch.Tensor, norm_dtype=torch.float16) -> TurboQuantProdState:
+        """``quantize`` (:4597-4666): a fresh state of the vectors' length (norms
+        f16, as the reference stores them)."""
+        B, H, L, _ = vectors.shape
+        st = self.alloc(B, H, L, vectors.device, norm_dtype)
+        self.quantize_into(vectors, st, 0)
+        return st
+
+    def dequantize(self, state: TurboQuantProdState) -> torch.Tensor:
+        """``dequantize`` (:4668-4677): f32 (B, H, T, D)."""
+        _require_device(*state)
+        B, H, T = state.norms.shape
+        cap = _capacity_of(state.norms, state.qjl_signs, self.sign_width)
+        if self.mse_bits > 0 and _capacity_of(state.norms, state.mse_indices, self.mse_width) != cap:
+            raise ValueError("Prod state buffers must share a capacity")
+        out = torch.empty((B, H, T, self.dim), dtype=torch.float32, device=state.norms.device)
+        dt = self.device_tensors(out.device)
+        lib = _lib.load()
+        rc = lib.tq_prod_dequantize(
+            state.norms.data_ptr(), state.mse_indices.data_ptr() if self.mse_bits > 0 else None,
+            state.residual_norms.data_ptr(), state.qjl_signs.data_ptr(),
+            _lib.torch_dtype_code(state.norms.dtype), B, H, T, self.dim, self.bits, cap,
+            dt["signs"].data_ptr(), dt["codebook"].data_ptr(), dt["projection"].data_ptr(),
+            out.data_ptr(), _stream(out))
+        _lib.check(rc, "tq_prod_dequantize")
+        return out

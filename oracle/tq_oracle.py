@@ -367,6 +367,118 @@ def dequantize(packed: np.ndarray, norms: np.ndarray, bits: int, dim: int,
 
 
 # ---------------------------------------------------------------------------
+# Prod codec: MSE at bits - 1 plus a 1-bit QJL sketch of the residual
+# (_TurboQuantProdCodec, turboquant_cache.py:4572-4766)
+# ---------------------------------------------------------------------------
+def projection_matrix(dim: int, seed: int) -> np.ndarray:
+    """Gaussian QJL projection (``_projection_matrix``, :3579-3584); the codec
+    draws it with ``seed + 1`` (:4577)."""
+    rng = np.random.default_rng(seed + dim * 2971 + 17)
+    return rng.standard_normal((dim, dim), dtype=np.float32)
+
+
+def prod_scale(dim: int) -> np.float32:
+    """``sqrt(pi / 2) / dim`` (:4584), as the f32 ``scale_array`` the kernels read."""
+    return np.float32(math.sqrt(math.pi / 2) / dim)
+
+
+def quantize_prod(x: np.ndarray, bits: int, signs: np.ndarray, mse_codebook: Optional[np.ndarray],
+                  proj: np.ndarray, norm_dtype: str = "float32"):
+    """Array path of ``_TurboQuantProdCodec.quantize`` (:4653-4666) in f32.
+
+    ``n = ||x||``, ``u = x / max(n, 1e-6)``; the MSE codec at ``bits - 1``
+    quantizes ``u`` (indices as ``quantize_rht``) and its estimate is
+    ``R^-1(c[idx])`` (``_quantize_unit_with_estimate``, :4149-4166); the
+    residual ``u - estimate`` keeps its norm and the signs of
+    ``residual @ P^T`` (``>= 0`` -> 1), packed one bit each.  With
+    ``bits == 1`` there is no MSE part and the residual is ``u``.
+    Returns (norms, mse_packed, residual_norms, sign_packed, projected): the
+    f32 ``projected`` lets tests bound sign flips near zero, where the order
+    of a matrix product's sum decides.
+    """
+    xf = np.asarray(x, np.float32)
+    n = norm_f32(xf)
+    u = xf / np.maximum(n, EPS)[..., None]
+    mb = bits - 1
+    if mb >= 1:
+        y = rht_forward_f32(u, signs)
+        idx = quantize_indices(y, midpoints(mse_codebook))
+        mse_packed = pack_lowbit(idx, mb)
+        est = rht_inverse_f32(mse_codebook.astype(np.float32)[idx], signs)
+        residual = (u - est).astype(np.float32)
+    else:
+        mse_packed = np.zeros((*xf.shape[:-1], 0), np.uint32)
+        residual = u
+    rn = norm_f32(residual)
+    projected = (residual.astype(np.float64) @ proj.astype(np.float64).T).astype(np.float32)
+    sign_packed = pack_lowbit((projected >= 0).astype(np.uint32), 1)
+    return (round_to_dtype(n, norm_dtype), mse_packed, round_to_dtype(rn, norm_dtype), sign_packed,
+            projected)
+
+
+def prod_key_vectors(norms, mse_packed, residual_norms, sign_packed, *, bits: int, dim: int,
+                     signs: np.ndarray, mse_codebook: Optional[np.ndarray],
+                     proj: np.ndarray) -> np.ndarray:
+    """Dequantized keys ``n * (R^-1 c[idx] + scale * rn * (s @ P))`` in float64
+    (``_TurboQuantProdCodec.dequantize``, :4668-4677), with s = +-1 from the bits."""
+    n = np.asarray(norms, np.float64)[..., None]
+    rn = np.asarray(residual_norms, np.float64)[..., None]
+    s = unpack_lowbit(sign_packed, 1, dim).astype(np.float64) * 2.0 - 1.0
+    qjl = float(prod_scale(dim)) * rn * (s @ proj.astype(np.float64))
+    if bits - 1 >= 1:
+        idx = unpack_lowbit(mse_packed, bits - 1, dim)
+        mse = rht_inverse_f64(mse_codebook.astype(np.float64)[idx], signs)
+    else:
+        mse = 0.0
+    return n * (mse + qjl)
+
+
+def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: np.ndarray,
+                   v_norms: np.ndarray, *, k_bits: int, v_bits: int, k_signs_rot: np.ndarray,
+                   k_mse_codebook: Optional[np.ndarray], proj: np.ndarray,
+                   v_codebook: np.ndarray, v_rot: np.ndarray, scale: float, q_dtype: str,
+                   causal: bool = False, lengths: Optional[Sequence[int]] = None) -> np.ndarray:
+    """Attention with Prod-coded keys and MSE-coded values, float64.
+
+    Scores follow ``score_prepared`` (:4700-4766) -- ``n * q_rot . c[idx] +
+    n * scale * rn * (q_proj . s)`` with ``q_rot = R_K q_s`` and ``q_proj =
+    q_s @ P^T`` (``prepare_queries``, :4692-4698) -- which is what the
+    fused Prod decode kernel computes per token (:2000-2206); the rest is
+    ``quantized_attention`` (:5110-5203) as in ``attention``.  Evaluated on
+    the dequantized keys, which is the same bilinear form.
+    """
+    B, Hq, L, D = q.shape
+    Hkv = np.asarray(k_norms).shape[1]
+    R = Hq // Hkv
+    qs = scale_queries(q, scale, q_dtype).astype(np.float64)
+    kd_all = prod_key_vectors(k_norms, k_mse, k_rnorms, k_signs, bits=k_bits, dim=D,
+                              signs=k_signs_rot, mse_codebook=k_mse_codebook, proj=proj)
+    vc = v_codebook.astype(np.float64)
+    out = np.zeros((B, Hq, L, D), np.float64)
+    fmin = float(np.finfo(np.float32).min)
+    cap = kd_all.shape[2]
+    for b in range(B):
+        T = cap if lengths is None else int(lengths[b])
+        if T == 0:
+            continue
+        for g in range(Hkv):
+            kd = kd_all[b, g, :T]
+            vidx = unpack_lowbit(v_packed[b, g, :T], v_bits, D)
+            vd = vc[vidx] * np.asarray(v_norms[b, g, :T], np.float64)[:, None]
+            for r in range(R):
+                h = g * R + r
+                s = qs[b, h] @ kd.T
+                if causal:
+                    qi = (T - L) + np.arange(L)[:, None]
+                    s = np.where(qi >= np.arange(T)[None, :], s, fmin)
+                m = s.max(axis=-1, keepdims=True)
+                p = np.exp(s - m)
+                l = p.sum(axis=-1, keepdims=True)
+                out[b, h] = rht_inverse_f64(p @ vd, v_rot) / np.maximum(l, float(EPS))
+    return out
+
+
+# ---------------------------------------------------------------------------
 # a11-a15: attention over the packed cache
 # ---------------------------------------------------------------------------
 def scale_queries(q: np.ndarray, scale: float, q_dtype: str) -> np.ndarray:

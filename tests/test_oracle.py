@@ -308,3 +308,74 @@ def test_bf16_rounding_matches_torch():
     x = np.random.default_rng(5).standard_normal(10000).astype(np.float32) * 100
     want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(O.round_to_dtype(x, "bf16"), want)
+
+
+# ---------------------------------------------------------------- Prod codec
+def test_prod_projection_matrix_is_the_seeded_gaussian():
+    """``_projection_matrix`` (:3579-3584): default_rng(seed + 2971 d + 17)."""
+    p = O.projection_matrix(64, 1)
+    assert p.dtype == np.float32 and p.shape == (64, 64)
+    ref = np.random.default_rng(1 + 64 * 2971 + 17).standard_normal((64, 64), dtype=np.float32)
+    assert np.array_equal(p, ref)
+    assert abs(float(p.mean())) < 0.05 and abs(float(p.std()) - 1.0) < 0.05
+    assert not np.array_equal(O.projection_matrix(64, 2), p)
+
+
+def test_prod_quantize_parts_against_closed_forms():
+    """MSE part = quantize_rht at bits - 1; the estimate and residual agree with
+    the Sylvester-matrix float64 forms; one bit = pure QJL of u."""
+    from scipy.linalg import hadamard
+
+    rng = np.random.default_rng(4)
+    d = 64
+    x = rng.standard_normal((3, 2, 7, d)).astype(np.float32)
+    sg = O.rht_signs(d, 0)
+    cb = O.beta_codebook(d, 2)
+    n, mse, rn, packed_signs, proj = O.quantize_prod(x, 3, sg, cb, O.projection_matrix(d, 1))
+    wp, wn = O.quantize_rht(x, 2, sg, cb)
+    assert np.array_equal(mse, wp) and np.array_equal(n, wn)
+    u = x.astype(np.float64) / np.maximum(n, 1e-6)[..., None]
+    idx = O.unpack_lowbit(mse, 2, d)
+    Hm = hadamard(d).astype(np.float64) / np.sqrt(d)
+    est = (cb.astype(np.float64)[idx] @ Hm.T) * sg       # R^-1 c = s * (H c) / sqrt(d)
+    res = u - est
+    np.testing.assert_allclose(rn, np.linalg.norm(res, axis=-1), rtol=1e-5)
+    np.testing.assert_allclose(proj, res @ O.projection_matrix(d, 1).astype(np.float64).T,
+                               rtol=1e-4, atol=1e-5)
+    # one bit: no MSE part, the residual is the unit vector
+    n1, mse1, rn1, _, _ = O.quantize_prod(x, 1, sg, None, O.projection_matrix(d, 1))
+    assert mse1.shape[-1] == 0
+    np.testing.assert_allclose(rn1, 1.0, rtol=1e-6)
+
+
+def test_prod_signs_follow_the_projection_rows():
+    """A permutation projection makes the signs the permuted residual's
+    signs (catches a transposed P) and ties at zero give 1 (``>= 0``)."""
+    d = 64
+    rng = np.random.default_rng(6)
+    perm = rng.permutation(d)
+    P = np.zeros((d, d), np.float32)
+    P[np.arange(d), perm] = 1.0                          # (P r)_j = r[perm[j]]
+    x = rng.standard_normal((5, d)).astype(np.float32)
+    _, _, _, sg, proj = O.quantize_prod(x, 1, O.rht_signs(d, 0), None, P)
+    u = x / O.norm_f32(x)[:, None]
+    assert np.array_equal(O.unpack_lowbit(sg, 1, d), (u[:, perm] >= 0).astype(np.uint32))
+    _, _, _, sg0, _ = O.quantize_prod(np.zeros((1, d), np.float32), 1, O.rht_signs(d, 0), None, P)
+    assert O.unpack_lowbit(sg0, 1, d).all()              # zero residual: every sign bit set
+
+
+def test_prod_dequantize_is_an_unbiased_inner_product():
+    """QJL scale sqrt(pi/2)/d and orientation s @ P: the regression slope of
+    <q, k_hat> on <q, k> is 1 (a wrong scale or P^T would move it)."""
+    rng = np.random.default_rng(8)
+    d = 64
+    k = rng.standard_normal((1, 1, 3000, d)).astype(np.float32)
+    q = rng.standard_normal(d)
+    sg, P = O.rht_signs(d, 0), O.projection_matrix(d, 1)
+    n, mse, rn, bits_, _ = O.quantize_prod(k, 2, sg, O.beta_codebook(d, 1), P)
+    kh = O.prod_key_vectors(n, mse, rn, bits_, bits=2, dim=d, signs=sg,
+                            mse_codebook=O.beta_codebook(d, 1), proj=P)[0, 0]
+    exact = k[0, 0].astype(np.float64) @ q
+    est = kh @ q
+    slope = float(est @ exact / (exact @ exact))
+    assert abs(slope - 1.0) < 0.04, slope
