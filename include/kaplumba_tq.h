@@ -43,7 +43,7 @@ enum {
 /* ---- enums ------------------------------------------------------------- */
 enum { TQ_DTYPE_F32 = 0, TQ_DTYPE_F16 = 1, TQ_DTYPE_BF16 = 2 };
 enum { TQ_ROT_HADAMARD = 0, TQ_ROT_DENSE = 1 };
-enum { TQ_KV_PACKED = 0, TQ_KV_PLAIN = 1 };
+enum { TQ_KV_PACKED = 0, TQ_KV_PLAIN = 1, TQ_KV_PROD = 2 /* tq_attention_prod keys */ };
 
 /* Library version string, e.g. "kaplumba_tq 0.1.0 gfx950". */
 const char* tq_version(void);
@@ -225,6 +225,29 @@ int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int 
                         int64_t capacity, int64_t max_tokens, const int32_t* seq_starts,
                         const int32_t* seq_lens, int causal,
                         void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Decode / verify attention with Prod-coded keys (tq_prod_quantize) and
+ * MSE-coded values.  Replaces the fused Prod decode kernel
+ * (_fully_fused_decode_kernel, tq.py:2000-2206) and quantized_attention
+ * with a Prod key codec (score_prepared, tq.py:4700-4766):
+ *   s_t = n_t (R_K q_s) . c[idx_t] + n_t rn_t sqrt(pi/2)/dim (q_s @ P^T) . sgn_t
+ * with sgn = +-1 from the sign bits; softmax, value sum, R_V^-1 and the
+ * causal / ragged / left-padding rules as tq_attention_ranged.
+ * k_bits is the Prod width (2..4; the MSE part k_mse has k_bits - 1 bits).
+ * Built for dim 64 / 128 and at most 4 query rows per kv head (Hq/Hkv * L);
+ * other shapes return TQ_ERR_UNSUPPORTED.  Workspace as tq_attention.
+ */
+int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                      int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
+                      const void* k_mse, const void* k_norms, const void* k_signs,
+                      const void* k_residual_norms, int k_bits, const float* k_mse_codebook,
+                      const float* k_rot_signs, const float* projection,
+                      const void* v, const void* v_norms, int v_bits, const float* v_codebook,
+                      const float* v_rot_signs, int norm_dtype, int64_t capacity,
+                      int64_t max_tokens, const int32_t* seq_starts, const int32_t* seq_lens,
+                      int causal, void* out, void* workspace, int64_t workspace_bytes,
+                      void* stream);
 
 #ifdef __cplusplus
 }

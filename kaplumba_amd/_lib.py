@@ -72,6 +72,14 @@ SIGNATURES = {
         c_int, c_void_p, c_void_p,                             # rot_kind, k_rot, v_rot
         c_int64, c_int64, c_void_p, c_int,                     # capacity, max_tokens, seq_lens, causal
         c_void_p, c_void_p, c_int64, c_void_p]),               # out, workspace, ws bytes, stream
+    "tq_attention_prod": (c_int, [
+        c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,   # q, dtype, B, Hq, Hkv, L, dim
+        c_int64, c_int64, c_int64, c_float,                    # q strides, scale
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,         # k mse, norms, signs, rnorms, k_bits
+        c_void_p, c_void_p, c_void_p,                          # k mse codebook, k rot signs, P
+        c_void_p, c_void_p, c_int, c_void_p, c_void_p,         # v, v_norms, v_bits, v codebook, v signs
+        c_int, c_int64, c_int64, c_void_p, c_void_p, c_int,    # norm dtype, cap, T, starts, lens, causal
+        c_void_p, c_void_p, c_int64, c_void_p]),               # out, workspace, ws bytes, stream
     "tq_attention_ranged": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
         c_int64, c_int64, c_int64, c_float,

@@ -60,6 +60,11 @@ struct AttnParams {
   float* po;           // [B, Hq, L, n_splits, D]
   float* pml;          // [B, Hq, L, n_splits, 2]
   float rscale;        // f32(1/sqrt(D))
+  // Prod-coded keys (kv kind TQ_KV_PROD): k / kn are the MSE part at bits - 1
+  const void* ksg;     // QJL sign rows [B, Hkv, cap, D / 32] u32
+  const void* krn;     // residual norms [B, Hkv, cap] (norm_dtype)
+  const float* qproj;  // q_s @ P^T rows [B, Hq, L, D] (workspace, from qprep_kernel)
+  float qjl_scale;     // f32(sqrt(pi / 2) / D)
   // output
   void* out;
 };

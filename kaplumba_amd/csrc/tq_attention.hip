@@ -175,16 +175,25 @@ extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, in
                   workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, false), B, Hq, Hkv, L, dim));
 }
 
-extern "C" int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
-                                   int dim, int64_t q_stride_b, int64_t q_stride_h,
-                                   int64_t q_stride_l, float scale, int kv_kind, int kv_dtype,
-                                   const void* k, const void* k_norms, const void* v,
-                                   const void* v_norms, int norm_dtype, int k_bits, int v_bits,
-                                   const float* k_codebook, const float* v_codebook, int rot_kind,
-                                   const float* k_rot, const float* v_rot, int64_t capacity,
-                                   int64_t max_tokens, const int32_t* seq_starts,
-                                   const int32_t* seq_lens, int causal, void* out, void* workspace,
-                                   int64_t workspace_bytes_given, void* stream) {
+namespace {
+
+// The key side of Prod-coded keys (tq_attention_prod); k / k_norms carry the
+// MSE part at k_bits = bits - 1.
+struct ProdKeys {
+  const void* signs;
+  const void* rnorms;
+  const float* proj;
+};
+
+int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                   int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
+                   int kv_kind, int kv_dtype, const void* k, const void* k_norms, const void* v,
+                   const void* v_norms, int norm_dtype, int k_bits, int v_bits,
+                   const float* k_codebook, const float* v_codebook, int rot_kind,
+                   const float* k_rot, const float* v_rot, int64_t capacity, int64_t max_tokens,
+                   const int32_t* seq_starts, const int32_t* seq_lens, int causal, void* out,
+                   void* workspace, int64_t workspace_bytes_given, void* stream,
+                   const ProdKeys* prod) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || L < 1 || Hq % Hkv)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bad heads/L (Hq %d, Hkv %d, L %d)", Hq, Hkv, L);
   if (dim != 64 && dim != 128 && dim != 256)
@@ -196,7 +205,20 @@ extern "C" int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, in
   if (max_tokens < 0 || max_tokens > capacity)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: max_tokens %lld > capacity %lld",
                 (long long)max_tokens, (long long)capacity);
-  if (kv_kind == TQ_KV_PACKED) {
+  if (prod) {
+    // Prod keys: the small row-group kernel (<= 4 query rows per kv head, d <= 128)
+    if (dim > 128 || static_cast<int64_t>(Hq / Hkv) * L > 4)
+      return fail(TQ_ERR_UNSUPPORTED, "attention: Prod keys need d <= 128 and at most 4 query rows "
+                  "per kv head (got d %d, %d rows)", dim, (Hq / Hkv) * L);
+    if (k_bits < 1 || k_bits > 3)
+      return fail(TQ_ERR_UNSUPPORTED, "attention: Prod keys of %d bits (2..4 are built)", k_bits + 1);
+    if (rot_kind != TQ_ROT_HADAMARD)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: Prod keys use the Hadamard rotation");
+    if (max_tokens > 0 && (!prod->signs || !prod->rnorms))
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null Prod key pointer");
+    if (!prod->proj) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null projection matrix");
+  }
+  if (kv_kind == TQ_KV_PACKED || kv_kind == TQ_KV_PROD) {
     if (k_bits < 1 || k_bits > 4 || v_bits < 1 || v_bits > 4)
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bits k=%d v=%d not in 1..4", k_bits, v_bits);
     if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
@@ -288,6 +310,21 @@ extern "C" int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   p.rscale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
   int rc = TQ_OK;
+  if (prod) {
+    // q_proj = q_s @ P^T into the rotated-query region (unused by the Hadamard rotation)
+    p.ksg = prod->signs;
+    p.krn = prod->rnorms;
+    p.qproj = p.qrot;
+    p.qjl_scale = static_cast<float>(__builtin_sqrt(3.14159265358979323846 / 2.0) / dim);
+    AttnParams pq = p;
+    pq.krot = prod->proj;
+    switch (dim) {
+      case 64: launch_qprep<64>(pq, q_dtype, rows, st); break;
+      default: launch_qprep<128>(pq, q_dtype, rows, st); break;
+    }
+    rc = check_launch("qprep_kernel (q @ P^T)");
+    if (rc) return rc;
+  }
   if (kv_kind == TQ_KV_PACKED && rot_kind == TQ_ROT_DENSE) {
     switch (dim) {
       case 64: launch_qprep<64>(p, q_dtype, rows, st); break;
@@ -317,6 +354,27 @@ extern "C" int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, in
   return check_launch("attn_merge_kernel");
 }
 
+}  // namespace
+
+extern "C" int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
+                                   int dim, int64_t q_stride_b, int64_t q_stride_h,
+                                   int64_t q_stride_l, float scale, int kv_kind, int kv_dtype,
+                                   const void* k, const void* k_norms, const void* v,
+                                   const void* v_norms, int norm_dtype, int k_bits, int v_bits,
+                                   const float* k_codebook, const float* v_codebook, int rot_kind,
+                                   const float* k_rot, const float* v_rot, int64_t capacity,
+                                   int64_t max_tokens, const int32_t* seq_starts,
+                                   const int32_t* seq_lens, int causal, void* out, void* workspace,
+                                   int64_t workspace_bytes_given, void* stream) {
+  if (kv_kind != TQ_KV_PACKED && kv_kind != TQ_KV_PLAIN)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: kv_kind %d", kv_kind);
+  return attention_impl(q, q_dtype, B, Hq, Hkv, L, dim, q_stride_b, q_stride_h, q_stride_l, scale,
+                        kv_kind, kv_dtype, k, k_norms, v, v_norms, norm_dtype, k_bits, v_bits,
+                        k_codebook, v_codebook, rot_kind, k_rot, v_rot, capacity, max_tokens,
+                        seq_starts, seq_lens, causal, out, workspace, workspace_bytes_given, stream,
+                        nullptr);
+}
+
 extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
                             int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l,
                             float scale, int kv_kind, int kv_dtype, const void* k,
@@ -331,4 +389,23 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
                              v_bits, k_codebook, v_codebook, rot_kind, k_rot, v_rot, capacity,
                              max_tokens, nullptr, seq_lens, causal, out, workspace,
                              workspace_bytes_given, stream);
+}
+
+extern "C" int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                                 int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l,
+                                 float scale, const void* k_mse, const void* k_norms,
+                                 const void* k_signs, const void* k_residual_norms, int k_bits,
+                                 const float* k_mse_codebook, const float* k_rot_signs,
+                                 const float* projection, const void* v, const void* v_norms,
+                                 int v_bits, const float* v_codebook, const float* v_rot_signs,
+                                 int norm_dtype, int64_t capacity, int64_t max_tokens,
+                                 const int32_t* seq_starts, const int32_t* seq_lens, int causal,
+                                 void* out, void* workspace, int64_t workspace_bytes_given,
+                                 void* stream) {
+  const ProdKeys pk{k_signs, k_residual_norms, projection};
+  return attention_impl(q, q_dtype, B, Hq, Hkv, L, dim, q_stride_b, q_stride_h, q_stride_l, scale,
+                        TQ_KV_PROD, 0, k_mse, k_norms, v, v_norms, norm_dtype, k_bits - 1, v_bits,
+                        k_mse_codebook, v_codebook, TQ_ROT_HADAMARD, k_rot_signs, v_rot_signs,
+                        capacity, max_tokens, seq_starts, seq_lens, causal, out, workspace,
+                        workspace_bytes_given, stream, &pk);
 }

@@ -52,9 +52,32 @@ int launch_partial_vb(const AttnParams& p, int vb, hipStream_t st) {
   return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
 }
 
+// Prod-coded keys (MSE part kb = bits - 1 >= 1): the small row-group kernel only.
+template <int D, int KB>
+int launch_prod_vb(const AttnParams& p, int vb, hipStream_t st) {
+  switch (vb) {
+    case 1: return launch_small<D, KB, 1, true>(p, st);
+    case 2: return launch_small<D, KB, 2, true>(p, st);
+    case 3: return launch_small<D, KB, 3, true>(p, st);
+    case 4: return launch_small<D, KB, 4, true>(p, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
+}
+
 template <int D>
 int launch_partial_dim(const AttnParams& p, int kv_kind, int kv_dtype, int kb, int vb,
                        hipStream_t st) {
+  if (kv_kind == TQ_KV_PROD) {
+    if constexpr (D <= 128) {
+      switch (kb) {
+        case 1: return launch_prod_vb<D, 1>(p, vb, st);
+        case 2: return launch_prod_vb<D, 2>(p, vb, st);
+        case 3: return launch_prod_vb<D, 3>(p, vb, st);
+      }
+      return fail(TQ_ERR_UNSUPPORTED, "attention: Prod keys need an MSE part of 1..3 bits, got %d", kb);
+    }
+    return fail(TQ_ERR_UNSUPPORTED, "attention: Prod keys at head dim %d (64 / 128 are built)", D);
+  }
   if (kv_kind == TQ_KV_PLAIN) {
     if (kv_dtype == TQ_DTYPE_F16) return launch_plain<D, TQ_DTYPE_F16>(p, st);
     if (kv_dtype == TQ_DTYPE_BF16) return launch_plain<D, TQ_DTYPE_BF16>(p, st);

@@ -233,6 +233,16 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   for (int i = 0; i < (1 << KB); ++i) ckb[i] = p.kcb[i];
 #pragma unroll
   for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
+  // f16 norms with an odd slab end: the last token's norms are read with
+  // 2-byte loads (the 16-byte load reads the dword that also spans token
+  // t_end as zero) and patched in its sub-chunk's slow path
+  const bool odd_tail = nf16 && (t_end & 1);
+  uint32_t tail_k = 0, tail_v = 0;
+  if (odd_tail) {
+    const uint32_t off = static_cast<uint32_t>(t_end - 1) * 2u;
+    tail_k = __builtin_amdgcn_raw_buffer_load_b16(knrs, off, 0, 0);
+    tail_v = __builtin_amdgcn_raw_buffer_load_b16(vnrs, off, 0, 0);
+  }
   Buf buf[P];
 #pragma unroll
   for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
@@ -445,6 +455,17 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     const bool edge = s0 + SUB > t_end || s0 + SUB - 1 > lim_min;  // wave-uniform
     if (edge || __any((dmax > kLazy || nvmax > nv_lim) ? 1 : 0)) {
       // ---- slow path: masks, new reference max / norm exponent, rescale
+      if (odd_tail && edge) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (s0 + 16 * (k >> 2) + 4 * g + (k & 3) == t_end - 1) {
+            nk[k] = f16_bits_to_f32(static_cast<uint16_t>(tail_k));
+            nv[k] = f16_bits_to_f32(static_cast<uint16_t>(tail_v));
+          }
+        nvmax = nv[0];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) nvmax = fmaxf(nvmax, nv[k]);
+      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         sc[k] *= nk[k] * kscale;

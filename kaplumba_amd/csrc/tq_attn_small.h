@@ -51,7 +51,7 @@
 
 namespace tq {
 
-template <int D, int KB, int VB>
+template <int D, int KB, int VB, bool PROD = false>
 struct SmallShape {
   static constexpr int NW = 8;
   static constexpr int NT = NW * kWave;
@@ -80,17 +80,24 @@ struct SmallShape {
   static constexpr int VKEYS = 1 << (2 * VB);
   static constexpr int REPV = VKEYS <= 64 ? 64 : 16;
   static constexpr int LOGSV = REPV == 64 ? 9 : 7;  // log2(REPV * 8): (hi pair, lo pair) entries
-  // LDS (bytes): [K hi table][K lo table][V (hi, lo) table][q staging][zeros][row max]
+  // Prod-coded keys (PROD): a second query set (q_proj) against one-bit QJL
+  // signs, looked up in a table of (+-1, +-1) f16 pairs
+  static constexpr int NQS = PROD ? 2 : 1;      // query sets
+  static constexpr int SW = PROD ? D / 64 : 1;  // sign words per lane (half a row)
+  static constexpr int STAB = PROD ? 4 * 64 * 4 : 0;
+  // LDS (bytes): [sign table][K hi table][K lo table][V (hi, lo) table][q staging][zeros][rows][row max]
   static constexpr int KTAB = KKEYS * REPK * 4;
   static constexpr int VTAB = VKEYS * REPV * 8;
-  static constexpr int LUTK_OFF = 0;
-  static constexpr int LUTV_OFF = 2 * KTAB;
-  static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [p][r][h][i] 8 x f16 = 16 B
-  static constexpr int QST_BYTES = 2 * NQ * 2 * NKI * 16;
-  static constexpr int ZERO_OFF = QST_OFF + QST_BYTES;  // 16 zero bytes
-  static constexpr int QY_OFF = ZERO_OFF + 16;          // [NQ][D] f32 rotated queries
-  static constexpr int QMAX_OFF = QY_OFF + NQ * D * 4;  // [NQ] f32
-  static constexpr int LOOP_BYTES = QMAX_OFF + 16;
+  static constexpr int SGN_OFF = 0;
+  static constexpr int LUTK_OFF = STAB;
+  static constexpr int LUTV_OFF = LUTK_OFF + 2 * KTAB;
+  static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [set][p][r][h][i] 8 x f16 = 16 B
+  static constexpr int QST_BYTES = NQS * 2 * NQ * 2 * NKI * 16;
+  static constexpr int ZBYTES = PROD ? NKI * 16 : 16;
+  static constexpr int ZERO_OFF = QST_OFF + QST_BYTES;        // ZBYTES zero bytes
+  static constexpr int QY_OFF = ZERO_OFF + ZBYTES;            // [set][NQ][D] f32 rotated queries
+  static constexpr int QMAX_OFF = QY_OFF + NQS * NQ * D * 4;  // [set][NQ] f32
+  static constexpr int LOOP_BYTES = QMAX_OFF + NQS * 16;
   // epilogue (after a barrier the loop's buffers are dead)
   static constexpr int WO_OFF = 0;                       // [NW][NQ][D] f32
   static constexpr int WM_OFF = WO_OFF + NW * NQ * D * 4;  // [NW][NQ]
@@ -191,9 +198,9 @@ __device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], const float (&s
   }
 }
 
-template <int D, int KB, int VB>
+template <int D, int KB, int VB, bool PROD = false>
 __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
-  using S = SmallShape<D, KB, VB>;
+  using S = SmallShape<D, KB, VB, PROD>;
   constexpr int NW = S::NW;
   constexpr int NT = S::NT;
   constexpr int SUB = S::SUB;
@@ -248,6 +255,11 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   const auto vrs = buffer_rsrc(static_cast<const char*>(p.v) + kvrow0 * (PWV * 4), tn * (PWV * 4));
   const auto knrs = buffer_rsrc(static_cast<const char*>(p.kn) + kvrow0 * nb, tn * nb);
   const auto vnrs = buffer_rsrc(static_cast<const char*>(p.vn) + kvrow0 * nb, tn * nb);
+  // Prod keys: QJL sign rows (D / 8 bytes) and residual norms
+  const auto srs = buffer_rsrc(PROD ? static_cast<const char*>(p.ksg) + kvrow0 * (D / 8) : nullptr,
+                               PROD ? tn * (D / 8) : 0u);
+  const auto rnrs = buffer_rsrc(PROD ? static_cast<const char*>(p.krn) + kvrow0 * nb : nullptr,
+                                PROD ? tn * nb : 0u);
 
   // ---- lane roles
   float lsg[6];  // -1 where lane bit k is set (Hadamard butterflies)
@@ -257,6 +269,7 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   const int rq = n & 3;         // query row of this lane's score column
   // keys: token 16 (g >> 1) + n, half g & 1
   const uint32_t k_lane = (16 * (g >> 1) + n) * (PWK * 4) + (g & 1) * (KW * 4);
+  const uint32_t s_lane = (16 * (g >> 1) + n) * (D / 8) + (g & 1) * (S::SW * 4);
   // norms: tokens 16 jq + 4 g .. + 3 of the sub-chunk
   const uint32_t n_lane = (16 * jq + 4 * g) * nb;
   // values: coordinates CPL n .. CPL n + CPL - 1 of tokens 4g + e, 16 + 4g + e
@@ -267,7 +280,8 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   const uint32_t lutv_lane = (lane % S::REPV) * 8;
   uint32_t kmask = (S::KKEYS - 1u) << S::LOGSK;
   uint32_t vmask = (S::VKEYS - 1u) << S::LOGSV;
-  asm volatile("" : "+s"(kmask), "+s"(vmask));
+  uint32_t smask = 3u << 8;
+  asm volatile("" : "+s"(kmask), "+s"(vmask), "+s"(smask));
 
   const int n_tok = t_end - t_begin;
   const int n_my = n_tok > wave * SUB ? (n_tok - wave * SUB + NW * SUB - 1) / (NW * SUB) : 0;
@@ -277,10 +291,17 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
     uint32_t k[KW];
     uint32_t nk[4], nv[4];
     uint32_t v[8][VRAW];
+    uint32_t sg[PROD ? S::SW : 1], rn[PROD ? 4 : 1];
   };
   auto load_sub = [&](Buf& bf, int s0) {
     const uint32_t t0 = static_cast<uint32_t>(s0);
     load_words<KW>(bf.k, krs, t0 * (PWK * 4) + k_lane);
+    if constexpr (PROD) {
+      load_words<S::SW>(bf.sg, srs, t0 * (D / 8) + s_lane);
+      const auto r = __builtin_amdgcn_raw_buffer_load_b128(rnrs, t0 * nb + n_lane, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bf.rn[e] = r[e];
+    }
     // 4 norms: 16 bytes (f32) or 8 bytes (f16, the upper two words unused);
     // one load shape for both keeps the buffers in registers
     const uint32_t no = t0 * nb + n_lane;
@@ -311,17 +332,20 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
 
   // ---- prologue loads first (query row of this wave, signs, codebooks), then
   // the pipeline's sub-chunks (loads complete in order)
-  const int qrow = wave;  // waves 0..NQ-1 rotate one query row each
-  const bool qok = qrow < nrows;
+  // waves 0..NQ-1 rotate one query row each; with Prod keys waves NQ..2NQ-1
+  // bring the projected rows q_proj (set 1, from qprep_kernel)
+  const bool qset1 = PROD && wave >= NQ;
+  const int qrow = PROD ? (wave & (NQ - 1)) : wave;
+  const bool qok = (!PROD || wave < 2 * NQ) && qrow < nrows;
   uint32_t qraw[QE];
   float sgn[QE];
   {
-    const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
+    const bool q32 = dense || qset1 || p.q_dtype == TQ_DTYPE_F32;
     const int64_t qb = !qok ? 0
-                       : dense ? row_qoff(qrow) * D
-                               : b * p.q_sb + static_cast<int64_t>(gk * p.R + p.row_head[qrow]) * p.q_sh +
-                                     static_cast<int64_t>(p.row_lpos[qrow]) * p.q_sl;
-    const void* qsrc = dense ? static_cast<const void*>(p.qrot) : p.q;
+                       : (dense || qset1) ? row_qoff(qrow) * D
+                                          : b * p.q_sb + static_cast<int64_t>(gk * p.R + p.row_head[qrow]) * p.q_sh +
+                                                static_cast<int64_t>(p.row_lpos[qrow]) * p.q_sl;
+    const void* qsrc = qset1 ? static_cast<const void*>(p.qproj) : dense ? static_cast<const void*>(p.qrot) : p.q;
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
       const int64_t i = qb + lane + e * kWave;
@@ -334,6 +358,19 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   for (int i = 0; i < (1 << KB); ++i) ckb[i] = p.kcb[i];
 #pragma unroll
   for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
+  // f16 norms with an odd slab end: the dword holding the last token's norm
+  // also spans token t_end, so the bounded 16-byte load reads it as zero
+  // (range checks are per dword).  That token's norms come from 2-byte loads
+  // here and replace the zeros in its sub-chunk (an edge sub-chunk, so the
+  // slow path).
+  const bool odd_tail = nf16 && (t_end & 1);
+  uint32_t tail_k = 0, tail_v = 0, tail_r = 0;
+  if (odd_tail) {
+    const uint32_t off = static_cast<uint32_t>(t_end - 1) * 2u;
+    tail_k = __builtin_amdgcn_raw_buffer_load_b16(knrs, off, 0, 0);
+    tail_v = __builtin_amdgcn_raw_buffer_load_b16(vnrs, off, 0, 0);
+    if constexpr (PROD) tail_r = __builtin_amdgcn_raw_buffer_load_b16(rnrs, off, 0, 0);
+  }
   Buf buf[P];
 #pragma unroll
   for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
@@ -378,28 +415,38 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
     uint4* d = reinterpret_cast<uint4*>(lds + S::LUTV_OFF) + vslot * 4;
     d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
   }
-  if (tid < 4) reinterpret_cast<uint32_t*>(lds + S::ZERO_OFF)[tid] = 0u;
+  if constexpr (PROD) {
+    // QJL sign pairs: key a | b << 1 -> (+-1, +-1), 64 replicas, 8 per thread
+    if (tid < 32) {
+      const int key = tid / 8;
+      const uint32_t e = pack_f16x2((key & 1) ? 1.f : -1.f, (key & 2) ? 1.f : -1.f);
+      uint4* d = reinterpret_cast<uint4*>(lds + S::SGN_OFF) + tid * 2;
+      d[0] = d[1] = make_uint4(e, e, e, e);
+    }
+  }
+  if (tid < S::ZBYTES / 4) reinterpret_cast<uint32_t*>(lds + S::ZERO_OFF)[tid] = 0u;
 
   // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
   // (dense: rotated by qprep_kernel), into LDS with the row's max |y|
-  if (wave < NQ) {
+  if (wave < NQ * S::NQS) {
     float y[QE];
-    const bool q32 = dense || p.q_dtype == TQ_DTYPE_F32;
+    const bool q32 = dense || qset1 || p.q_dtype == TQ_DTYPE_F32;
+    const bool asis = dense || qset1;  // rows already prepared by qprep_kernel
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
       const uint32_t raw = qraw[e];
       const float qv = q32 ? __builtin_bit_cast(float, raw)
                            : (p.q_dtype == TQ_DTYPE_F16 ? f16_bits_to_f32(static_cast<uint16_t>(raw))
                                                         : bf16_bits_to_f32(static_cast<uint16_t>(raw)));
-      y[e] = dense ? qv : round_q(p.q_dtype, qv * p.scale_q) * sgn[e];
+      y[e] = asis ? qv : round_q(p.q_dtype, qv * p.scale_q) * sgn[e];
     }
-    if (!dense) {
+    if (!asis) {
       wave_fwht<D>(y, lsg);
 #pragma unroll
       for (int e = 0; e < QE; ++e) y[e] *= p.rscale;
     }
     float m = 0.f;
-    float* qy = reinterpret_cast<float*>(lds + S::QY_OFF) + wave * D;
+    float* qy = reinterpret_cast<float*>(lds + S::QY_OFF) + wave * D;  // set 1 rows follow set 0
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
       qy[lane + e * kWave] = y[e];
@@ -413,22 +460,25 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   // q_p,r[h D/2 + 8 i + e], e = 0..7, as f16 (one hi/lo scale for all rows)
   const float* qmaxs = reinterpret_cast<const float*>(lds + S::QMAX_OFF);
   const float sq = f16_split_scale(fmaxf(fmaxf(qmaxs[0], qmaxs[1]), fmaxf(qmaxs[2], qmaxs[3])));
-  for (int idx = tid; idx < NQ * D; idx += NT) {
-    const int r = idx / D;
+  const float sqp = PROD ? f16_split_scale(fmaxf(fmaxf(qmaxs[4], qmaxs[5]), fmaxf(qmaxs[6], qmaxs[7]))) : 1.f;
+  for (int idx = tid; idx < S::NQS * NQ * D; idx += NT) {
+    const int set = idx / (NQ * D);
+    const int r = (idx / D) % NQ;
     const int c = idx % D;
     uint32_t hi, lo;
-    split_f16(reinterpret_cast<const float*>(lds + S::QY_OFF)[idx] * sq, hi, lo);
+    split_f16(reinterpret_cast<const float*>(lds + S::QY_OFF)[idx] * (set ? sqp : sq), hi, lo);
     const int h = c / (D / 2);
     const int i = (c % (D / 2)) / 8;
     const int e = c % 8;
     uint16_t* st = reinterpret_cast<uint16_t*>(lds + S::QST_OFF);
-    st[(((0 * NQ + r) * 2 + h) * NKI + i) * 8 + e] = static_cast<uint16_t>(hi);
-    st[(((1 * NQ + r) * 2 + h) * NKI + i) * 8 + e] = static_cast<uint16_t>(lo);
+    st[((((set * 2 + 0) * NQ + r) * 2 + h) * NKI + i) * 8 + e] = static_cast<uint16_t>(hi);
+    st[((((set * 2 + 1) * NQ + r) * 2 + h) * NKI + i) * 8 + e] = static_cast<uint16_t>(lo);
   }
   lds_barrier();
   // B operands: lane (column n = 8 p + 4 jq + rq, g) -- zero unless lane
   // group g holds tokens of subset jq
   u32x4_t qb[NKI];
+  uint32_t qb2_addr = 0;  // Prod keys: q_proj operands stay in LDS (registers are full)
   {
     const int pc = n >> 3;
     const bool on = (g >> 1) == jq;
@@ -436,9 +486,12 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < NKI; ++i)
       qb[i] = lds_at<u32x4_t>(lds, on ? base + i * 16 : static_cast<uint32_t>(S::ZERO_OFF));
+    if constexpr (PROD) qb2_addr = on ? base + 2 * NQ * 2 * NKI * 16 : static_cast<uint32_t>(S::ZERO_OFF);
   }
   // score scale: S * ||k|| * log2(e) / (s_K s_Q) in log2 units
   const float kscale = 1.4426950408889634f * __builtin_amdgcn_rcpf(sk) * __builtin_amdgcn_rcpf(sq);  // powers of two: exact
+  // Prod keys: the QJL term's scale sqrt(pi/2) / D * log2(e) / s_P (times n * rn per token)
+  const float kscale2 = PROD ? 1.4426950408889634f * p.qjl_scale * __builtin_amdgcn_rcpf(sqp) : 0.f;
   // causal limit of this lane's row (keys t <= lim are visible)
   int lim = INT32_MAX, lim_min = INT32_MAX;
   if (p.causal) {
@@ -463,9 +516,13 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   float nv_lim = 0.f;       // 2^(E + 8): larger norms could overflow an f16 weight
   float l_acc = 0.f;        // sum of p over this lane's tokens
 
-  // two independent accumulator chains (key hi parts, key lo parts)
-  auto scores = [&](const Buf& bf) -> f32x4_t {
-    f32x4_t Ch = {0.f, 0.f, 0.f, 0.f}, Cl = {0.f, 0.f, 0.f, 0.f};
+  // two independent accumulator chains (key hi parts, key lo parts); with
+  // Prod keys a third against the QJL signs (exact +-1 in f16) and q_proj
+  struct Sc {
+    f32x4_t c, c2;
+  };
+  auto scores = [&](const Buf& bf) -> Sc {
+    f32x4_t Ch = {0.f, 0.f, 0.f, 0.f}, Cl = {0.f, 0.f, 0.f, 0.f}, Cs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NKI; ++i) {
       u32x4_t ah, al;
@@ -477,11 +534,19 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
       }
       Ch = mfma_f16(ah, qb[i], Ch);
       Cl = mfma_f16(al, qb[i], Cl);
+      if constexpr (PROD) {
+        u32x4_t as;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          as[u] = lds_at<uint32_t>(lds, S::SGN_OFF + key_addr<2, 8>(bf.sg, 8 * i + 2 * u, (lane & 63) * 4u, smask));
+        Cs = mfma_f16(as, lds_at<u32x4_t>(lds, qb2_addr + i * 16), Cs);
+      }
     }
-    return Ch + Cl;
+    return Sc{Ch + Cl, Cs};
   };
 
-  auto finish = [&](const Buf& bf, f32x4_t C, int s0) {
+  auto finish = [&](const Buf& bf, const Sc& SC, int s0) {
+    const f32x4_t C = SC.c;
     // ---- value operands first (they do not depend on the softmax, and the
     // slow-path branch below would otherwise keep their table reads behind
     // it): pairs (4g, 4g+1), (4g+2, 4g+3), (16+4g, ..) of coordinate CPL n + c
@@ -518,21 +583,43 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
     float nk[4], nv[4], sc[4], d[4];
     norm4(bf.nk, nk);
     norm4(bf.nv, nv);
+    // Prod keys: score = n (q_rot . c[idx]) + n * rn * sqrt(pi/2)/D (q_proj . s)
+    float ks2[4], sc2[4];
+    if constexpr (PROD) {
+      float rn[4];
+      norm4(bf.rn, rn);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ks2[i] = nk[i] * rn[i] * kscale2;
+        const float ci = own_reg(SC.c2[i]);
+        sc2[i] = ci + __builtin_bit_cast(float, row_ror_u<8>(__builtin_bit_cast(uint32_t, ci)));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float ci = own_reg(C[i]);
       sc[i] = ci + __builtin_bit_cast(float, row_ror_u<8>(__builtin_bit_cast(uint32_t, ci)));
-      d[i] = fmaf(sc[i], nk[i] * kscale, -m_row);
+      d[i] = fmaf(sc[i], nk[i] * kscale, PROD ? fmaf(sc2[i], ks2[i], -m_row) : -m_row);
     }
     const float dmax = fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3]));
-    const float nvmax = fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3]));
+    float nvmax = fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3]));
     const bool edge = s0 + SUB > t_end || s0 + SUB - 1 > lim_min;  // wave-uniform
     if (edge || __any((dmax > kLazy || nvmax > nv_lim) ? 1 : 0)) {
       // ---- slow path: masks, new reference max / norm exponent, rescale
       const int tbase = s0 + 16 * jq + 4 * g;
+      if (odd_tail && edge) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (tbase + i == t_end - 1) {
+            nk[i] = f16_bits_to_f32(static_cast<uint16_t>(tail_k));
+            nv[i] = f16_bits_to_f32(static_cast<uint16_t>(tail_v));
+            if constexpr (PROD) ks2[i] = nk[i] * f16_bits_to_f32(static_cast<uint16_t>(tail_r)) * kscale2;
+          }
+        nvmax = fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3]));
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sc[i] *= nk[i] * kscale;
+        sc[i] = PROD ? fmaf(sc[i], nk[i] * kscale, sc2[i] * ks2[i]) : sc[i] * (nk[i] * kscale);
         if (edge) {
           if (tbase + i > lim) sc[i] = -FLT_MAX;
           if (tbase + i >= t_end) sc[i] = -INFINITY;
@@ -597,14 +684,14 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
 
   // Loads are issued unconditionally (past t_end they read zeros for free),
   // so the count of outstanding loads is exact for every sub-chunk.
-  f32x4_t Cn;
+  Sc Cn;
   if (n_my > 0) Cn = scores(buf[0]);
   for (int base = 0; base < n_my; base += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       const int i = base + s;
       if (i < n_my) {
-        const f32x4_t C = Cn;
+        const Sc C = Cn;
         finish(buf[s], C, sub_start(i));
         if (i + 1 < n_my) Cn = scores(buf[(s + 1) % P]);
       }
@@ -722,10 +809,10 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
   }
 }
 
-template <int D, int KB, int VB>
+template <int D, int KB, int VB, bool PROD = false>
 int launch_small(const AttnParams& p, hipStream_t st) {
   const dim3 grid(p.n_splits, p.Hkv, p.B);
-  hipLaunchKernelGGL((attn_small_kernel<D, KB, VB>), grid, dim3(SmallShape<D, KB, VB>::NT), 0, st, p);
+  hipLaunchKernelGGL((attn_small_kernel<D, KB, VB, PROD>), grid, dim3(SmallShape<D, KB, VB, PROD>::NT), 0, st, p);
   return check_launch("attn_small_kernel");
 }
 

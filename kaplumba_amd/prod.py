@@ -20,9 +20,9 @@ import torch
 
 from . import _lib
 from . import codebook as cbmod
-from .ops import Codec, _capacity_of, _require_device, _stream
+from .ops import (Codec, _capacity_of, _require_device, _seq_array, _stream, _workspace)
 
-__all__ = ["ProdCodec", "TurboQuantProdState"]
+__all__ = ["ProdCodec", "TurboQuantProdState", "attention_prod"]
 
 
 class TurboQuantProdState(NamedTuple):
@@ -128,3 +128,52 @@ class ProdCodec:
             out.data_ptr(), _stream(out))
         _lib.check(rc, "tq_prod_dequantize")
         return out
+
+
+def attention_prod(queries: torch.Tensor, keys: TurboQuantProdState, v_norms: torch.Tensor,
+                   v_idx: torch.Tensor, key_codec: ProdCodec, value_codec: Codec, scale: float,
+                   causal: bool, seq_lens: Optional[torch.Tensor] = None,
+                   seq_starts: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention with Prod-coded keys and MSE-coded values (``tq_attention_prod``):
+    the fused Prod decode kernel's scores (turboquant_cache.py:2000-2206) with
+    ``quantized_attention``'s softmax and masks.  Views (B, Hkv, T[, W]) of
+    contiguous capacity buffers, as the cache hands them out."""
+    _require_device(queries, *keys, v_norms, v_idx)
+    B, Hq, L, D = queries.shape
+    Hkv, T = keys.norms.shape[1], keys.norms.shape[2]
+    if key_codec.dim != D or value_codec.dim != D:
+        raise NotImplementedError("Prod attention needs equal query, key and value head dims")
+    if value_codec.rotation != "hadamard":
+        raise NotImplementedError("Prod attention pairs with Hadamard-rotated values")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} kv heads")
+    if queries.stride(-1) != 1:
+        queries = queries.contiguous()
+    cap = _capacity_of(keys.norms, keys.qjl_signs, key_codec.sign_width)
+    for nrm, idx, w in ((keys.norms, keys.mse_indices, key_codec.mse_width),
+                        (v_norms, v_idx, value_codec.packed_width)):
+        if w and _capacity_of(nrm, idx, w) != cap:
+            raise ValueError("key and value buffers must share a capacity")
+    if keys.residual_norms.shape != keys.norms.shape or keys.residual_norms.stride() != keys.norms.stride():
+        raise ValueError("residual norms must share the norms' layout")
+    if not (keys.norms.dtype == keys.residual_norms.dtype == v_norms.dtype):
+        raise ValueError("key norms, residual norms and value norms must share a dtype")
+    seq_lens = _seq_array(seq_lens, B, queries.device)
+    seq_starts = _seq_array(seq_starts, B, queries.device)
+    out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
+    lib = _lib.load()
+    ws = _workspace(queries.device, lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T))
+    kt, vt = key_codec.device_tensors(queries.device), value_codec.device_tensors(queries.device)
+    rc = lib.tq_attention_prod(
+        queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
+        queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
+        keys.mse_indices.data_ptr(), keys.norms.data_ptr(), keys.qjl_signs.data_ptr(),
+        keys.residual_norms.data_ptr(), key_codec.bits, kt["codebook"].data_ptr(),
+        kt["signs"].data_ptr(), kt["projection"].data_ptr(), v_idx.data_ptr(), v_norms.data_ptr(),
+        value_codec.bits, vt["codebook"].data_ptr(), vt["rot"].data_ptr(),
+        _lib.torch_dtype_code(v_norms.dtype), cap, T,
+        seq_starts.data_ptr() if seq_starts is not None else None,
+        seq_lens.data_ptr() if seq_lens is not None else None, 1 if causal else 0,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
+    _lib.check(rc, "tq_attention_prod")
+    return out

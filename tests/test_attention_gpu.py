@@ -212,6 +212,15 @@ def test_rows16_split_with_fully_masked_rows(device):
     run_case(device, 81, 1, 1, 1, 16, 9 * 256 + 2, 128, 3, 3, causal=True)
 
 
+@pytest.mark.parametrize("d,Hq,Hkv,L", [(128, 8, 2, 1), (64, 4, 2, 2), (128, 32, 8, 2), (256, 8, 2, 1)])
+def test_f16_norms_odd_sequence_ends(device, d, Hq, Hkv, L):
+    """f16 norms (the reference layout) with odd sequence ends: the last
+    token's norm shares a dword with the position past the end, which a
+    bounded 16-byte load reads as zero; the kernels must still use it."""
+    run_case(device, 90 + d + Hq + L, 3, Hq, Hkv, L, 701, d, 3, 3, qdt="f16", norm="float16",
+             lengths=[5, 701, 33])
+
+
 def test_empty_cache_gives_zeros(device):
     q = torch.randn(1, 8, 1, 128, dtype=torch.bfloat16, device=device)
     kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)

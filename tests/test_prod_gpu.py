@@ -103,3 +103,79 @@ def test_prod_inner_products_are_unbiased(device):
     assert abs(slope - 1.0) < 0.03, slope
     corr = np.corrcoef(est, exact)[0, 1]
     assert corr > 0.8, corr
+
+
+def _prod_case(device, seed, B, Hq, Hkv, L, T, d, kb, vb, qdt="bf16", lengths=None, starts=None,
+               causal=None, norm_dtype=torch.float32):
+    from kaplumba_amd import ops
+    from kaplumba_amd.prod import attention_prod
+    from tests import test_attention_gpu as _A
+    assert_close, q_tensor = _A.assert_close, _A.q_tensor
+
+    causal = (L > 1) if causal is None else causal
+    rng = np.random.default_rng(seed)
+    s = np.exp(rng.normal(0, 0.5, size=(1, Hkv, 1, d)))
+    k = (rng.standard_normal((B, Hkv, T, d)) * s).astype(np.float16)
+    v = (rng.standard_normal((B, Hkv, T, d)) * s).astype(np.float16)
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, d)).astype(np.float32), qdt)
+    kc, vc = ProdCodec(d, kb, 0), ops.Codec(d, vb, 1)
+    cap = T + 5
+    kst = kc.alloc(B, Hkv, cap, device, norm_dtype)
+    kc.quantize_into(torch.from_numpy(k).to(device), kst, 0)
+    vp = torch.zeros((B, Hkv, cap, vc.packed_width), dtype=torch.uint32, device=device)
+    vn = torch.zeros((B, Hkv, cap), dtype=norm_dtype, device=device)
+    ops.append_quantize(torch.from_numpy(v).to(device), vc, vp, vn, 0)
+    view = type(kst)(*(t[:, :, :T] for t in kst))
+    sl = torch.tensor(lengths, dtype=torch.int32) if lengths is not None else None
+    ss = torch.tensor(starts, dtype=torch.int32) if starts is not None else None
+    out = attention_prod(q_tensor(q, qdt, device), view, vn[:, :, :T], vp[:, :, :T], kc, vc,
+                         1 / np.sqrt(d), causal, seq_lens=sl, seq_starts=ss)
+    # the oracle reads the kernel-written state (its bits are checked above)
+    kn, km, kr, ks = (t[:, :, :T].float().cpu().numpy() if t.dtype != torch.uint32
+                      else t[:, :, :T].cpu().numpy().astype(np.uint32) for t in kst)
+    want = O.attention_prod(q, kn, km, kr, ks, vp[:, :, :T].cpu().numpy().astype(np.uint32),
+                            vn[:, :, :T].float().cpu().numpy(), k_bits=kb, v_bits=vb,
+                            k_signs_rot=O.rht_signs(d, 0), k_mse_codebook=O.beta_codebook(d, kb - 1),
+                            proj=O.projection_matrix(d, 1), v_codebook=O.beta_codebook(d, vb),
+                            v_rot=O.rht_signs(d, 1), scale=1 / np.sqrt(d), q_dtype=qdt,
+                            causal=causal, lengths=None if lengths is None else
+                            [min(x, T) for x in lengths]) if starts is None else None
+    if starts is not None:
+        parts = []
+        for b in range(B):
+            e = T if lengths is None else lengths[b]
+            sl_ = slice(starts[b], e)
+            parts.append(O.attention_prod(
+                q[b:b + 1], kn[b:b + 1, :, sl_], km[b:b + 1, :, sl_], kr[b:b + 1, :, sl_],
+                ks[b:b + 1, :, sl_], vp[b:b + 1, :, sl_].cpu().numpy().astype(np.uint32),
+                vn[b:b + 1, :, sl_].float().cpu().numpy(), k_bits=kb, v_bits=vb,
+                k_signs_rot=O.rht_signs(d, 0), k_mse_codebook=O.beta_codebook(d, kb - 1),
+                proj=O.projection_matrix(d, 1), v_codebook=O.beta_codebook(d, vb),
+                v_rot=O.rht_signs(d, 1), scale=1 / np.sqrt(d), q_dtype=qdt, causal=causal))
+        want = np.concatenate(parts)
+    assert_close(out, want, qdt, f"prod B{B} Hq{Hq} Hkv{Hkv} L{L} T{T} d{d} k{kb}v{vb}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("kb,vb", [(2, 1), (3, 3), (4, 2), (4, 4)])
+def test_prod_decode_attention(device, d, kb, vb):
+    _prod_case(device, 30 + d + kb * 10 + vb, 1, 8, 2, 1, 2500, d, kb, vb)
+
+
+def test_prod_verify_ragged_f16_norms(device):
+    """causal 2-draft verify (4 rows per kv head), ragged lengths, f16 norms, f16 queries."""
+    _prod_case(device, 7, 3, 4, 2, 2, 3000, 128, 3, 3, qdt="f16", lengths=[3000, 5, 1234],
+               norm_dtype=torch.float16)
+
+
+def test_prod_f16_norms_odd_sequence_ends(device):
+    _prod_case(device, 12, 3, 8, 2, 1, 701, 128, 4, 2, lengths=[5, 701, 33], norm_dtype=torch.float16)
+
+
+def test_prod_left_padded_rows(device):
+    _prod_case(device, 8, 2, 8, 2, 1, 2100, 128, 4, 3, starts=[0, 1500])
+
+
+def test_prod_rejects_unbuilt_shapes(device):
+    with pytest.raises(NotImplementedError):
+        _prod_case(device, 9, 1, 32, 8, 4, 300, 128, 3, 3)   # 16 rows per kv head
