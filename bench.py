@@ -396,6 +396,52 @@ def bench_prefill_attention(torch, args, dev):
             "prefill_tokens_per_s": round(L * 1e3 / ms, 1), "steps": steps}
 
 
+def bench_prod_decode(torch, args, dev):
+    """Config-1 decode with Prod-coded keys (3 bits: 2-bit MSE + one-bit QJL
+    signs, the TurboQuant inner-product codec) and 3-bit MSE values."""
+    from kaplumba_amd import ops
+    from kaplumba_amd.prod import ProdCodec, attention_prod
+
+    B, Hq, H, T, D = 1, CFG1["Hq"], CFG1["Hkv"], CFG1["T"], CFG1["D"]
+    kc, vc = ProdCodec(D, 3, 0), ops.Codec(D, 3, 1)
+    per_tok = 4 * kc.mse_width + 4 * kc.sign_width + 8 + 4 * vc.packed_width + 4
+    per_step = B * H * T * per_tok
+    n_sets = max(2, math.ceil(args.rotate_mb * 1e6 / per_step))
+    g = torch.Generator(device=dev).manual_seed(6000)
+    sets = []
+    for _ in range(n_sets):
+        k, v = _synth_kv(torch, g, (B, H, T, D), torch.float16, dev)
+        kst = kc.alloc(B, H, T, dev)
+        kc.quantize_into(k, kst, 0)
+        vp = torch.empty((B, H, T, vc.packed_width), dtype=torch.uint32, device=dev)
+        vn = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+        ops.append_quantize(v, vc, vp, vn, 0)
+        sets.append((kst, vn, vp))
+        del k, v
+    _free(torch)
+    qs = [torch.randn(B, Hq, 1, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(n_sets)]
+    scale = 1.0 / math.sqrt(D)
+
+    def step(i):
+        kst, vn, vp = sets[i % n_sets]
+        return attention_prod(qs[i % n_sets], kst, vn, vp, kc, vc, scale, False)
+
+    steps = max(5, args.steps // 4)
+    ms, outs, _ = graph_timed(torch, step, steps, max(2, args.warmup // 4), dev)
+    if not torch.equal(outs[0], step(0)):
+        raise RuntimeError("Prod decode: graph replay differs from the eager call")
+    del sets, outs
+    _free(torch)
+    gbs = per_step / (ms * 1e-3) / 1e9
+    return {"workload": "cfg1 decode with Prod keys: 3-bit Prod K (2-bit MSE + 1-bit QJL signs, "
+                        "f32 norm and residual norm) and 3-bit MSE V, 32 q / 8 kv heads, d=128, "
+                        "32768 tokens",
+            "value": round(gbs, 2), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "us_per_step": round(ms * 1e3, 3), "bytes_per_step": per_step,
+            "note": "one call = qprep_kernel (q @ P^T) + attn_small_kernel (Prod) + attn_merge_kernel",
+            "steps": steps}
+
+
 def cpu_baseline(seconds_budget=12.0):
     """Numpy restatement of the reference's array-path attention (oracle), cfg1 shape."""
     import numpy as np
@@ -440,9 +486,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=CFG1["T"],
                     help="cached tokens per kv head of the headline decode leg (context-length "
                          "sweeps; the config-1 figure is quoted at the default 32768)")
-    ap.add_argument("--legs", default="cfg0,cfg2,cfg3,cfg4,prefill",
+    ap.add_argument("--legs", default="cfg0,cfg2,cfg3,cfg4,prefill,prod",
                     help="comma-separated extra legs to run after the cfg1 headline "
-                         "(cfg0, cfg2, cfg3, cfg4, prefill; empty for the headline only)")
+                         "(cfg0, cfg2, cfg3, cfg4, prefill, prod; empty for the headline only)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -456,7 +502,7 @@ def main():
     dec = bench_decode(torch, args, dev)
     _free(torch)
     legs = {x.strip() for x in args.legs.split(",") if x.strip()}
-    unknown = legs - {"cfg0", "cfg2", "cfg3", "cfg4", "prefill"}
+    unknown = legs - {"cfg0", "cfg2", "cfg3", "cfg4", "prefill", "prod"}
     if unknown:
         ap.error(f"unknown legs: {sorted(unknown)}")
     value = dec["bytes"] / (dec["ms_per_step"] * 1e-3) / 1e9
@@ -503,6 +549,8 @@ def main():
         line["cfg4"] = bench_verify(torch, args, dev)
     if "prefill" in legs:
         line["prefill_attention"] = bench_prefill_attention(torch, args, dev)
+    if "prod" in legs:
+        line["prod_decode"] = bench_prod_decode(torch, args, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

@@ -22,9 +22,10 @@ import torch
 
 from . import ops
 from .codebook import DEFAULT_TURBOQUANT_SEED
+from .prod import ProdCodec, TurboQuantProdState, attention_prod
 
 __all__ = [
-    "TurboQuantMSEState", "TurboQuantKVCache", "KVCache", "make_prompt_cache",
+    "TurboQuantMSEState", "TurboQuantProdState", "TurboQuantKVCache", "KVCache", "make_prompt_cache",
     "save_prompt_cache", "load_prompt_cache", "can_trim_prompt_cache", "trim_prompt_cache",
     "create_attention_mask", "create_causal_mask",
 ]
@@ -144,6 +145,9 @@ class TurboQuantKVCache(_BaseCache):
                             reference), "hadamard" or "dense"
       codebook            : "beta" (reference) or "gaussian" (N(0,1) Lloyd-Max / sqrt(d))
       norm_dtype          : torch.float32 (default) or torch.float16 (reference layout)
+      key_quantizer       : "mse" (reference) or "prod": keys with the Prod codec
+                            (MSE at bits - 1 plus one-bit QJL signs of the residual,
+                            turboquant_cache.py:4572-4766), values stay MSE
     """
 
     decode_key_chunk_size = 1 << 30
@@ -159,12 +163,13 @@ class TurboQuantKVCache(_BaseCache):
     rotation = "auto"
     codebook_kind = "beta"
     norm_dtype = torch.float32
+    key_quantizer = "mse"
     _dims = (0, 0)
 
     def __init__(self, bits: float, seed: int = DEFAULT_TURBOQUANT_SEED, *,
                  key_bits: Optional[int] = None, val_bits: Optional[int] = None,
                  rotation: str = "auto", codebook: str = "beta",
-                 norm_dtype: torch.dtype = torch.float32):
+                 norm_dtype: torch.dtype = torch.float32, key_quantizer: str = "mse"):
         self.bits = _validate_bits(bits)
         self.seed = seed
         self.offset = 0
@@ -183,9 +188,14 @@ class TurboQuantKVCache(_BaseCache):
             raise ValueError(f"codebook must be 'beta' or 'gaussian', got {codebook!r}")
         if norm_dtype not in (torch.float32, torch.float16):
             raise ValueError("norm_dtype must be torch.float32 or torch.float16")
+        if key_quantizer not in ("mse", "prod"):
+            raise ValueError(f"key_quantizer must be 'mse' or 'prod', got {key_quantizer!r}")
+        if key_quantizer == "prod" and (rotation == "dense" or codebook != "beta"):
+            raise ValueError("Prod keys use the Hadamard rotation and the Beta codebook")
         self.rotation = rotation
         self.codebook_kind = codebook
         self.norm_dtype = norm_dtype
+        self.key_quantizer = key_quantizer
 
     # ------------------------------------------------------------ codecs ---
     @classmethod
@@ -208,7 +218,10 @@ class TurboQuantKVCache(_BaseCache):
     def _build_codecs(self, k_dim: int, v_dim: int) -> None:
         kb, vb = self._side_bits()
         if self.key_codec is None:
-            self.key_codec = ops.Codec(k_dim, kb, self.seed, self.rotation, self.codebook_kind)
+            if self.key_quantizer == "prod":
+                self.key_codec = ProdCodec(k_dim, kb, self.seed)
+            else:
+                self.key_codec = ops.Codec(k_dim, kb, self.seed, self.rotation, self.codebook_kind)
         if self.value_codec is None:
             self.value_codec = ops.Codec(v_dim, vb, self.seed + 1, self.rotation, self.codebook_kind)
 
@@ -224,7 +237,9 @@ class TurboQuantKVCache(_BaseCache):
             self._build_codecs(kd, vd)
 
     # ------------------------------------------------------------ storage ---
-    def _alloc(self, codec: ops.Codec, B: int, H: int, cap: int, device) -> TurboQuantMSEState:
+    def _alloc(self, codec, B: int, H: int, cap: int, device):
+        if isinstance(codec, ProdCodec):
+            return codec.alloc(B, H, cap, device, self.norm_dtype)
         return TurboQuantMSEState(
             torch.zeros((B, H, cap), dtype=self.norm_dtype, device=device),
             torch.zeros((B, H, cap, codec.packed_width), dtype=torch.uint32, device=device),
@@ -240,8 +255,8 @@ class TurboQuantKVCache(_BaseCache):
         B, H = st.norms.shape[:2]
         grown = self._alloc(codec, B, H, new_cap, st.norms.device)
         if self.offset > 0:
-            grown.norms[..., : self.offset].copy_(st.norms[..., : self.offset])
-            grown.indices[..., : self.offset, :].copy_(st.indices[..., : self.offset, :])
+            for dst, src in zip(grown, st):
+                dst[:, :, : self.offset].copy_(src[:, :, : self.offset])
         return grown
 
     def reserve(self, n_tokens: int, batch: int, n_kv_heads: int, k_dim: int, v_dim: int,
@@ -269,9 +284,14 @@ class TurboQuantKVCache(_BaseCache):
                                  f"{tuple(self.keys.norms.shape[:2])}")
             self.keys = self._grow(self.keys, self.key_codec, new_end)
             self.values = self._grow(self.values, self.value_codec, new_end)
-        ops.append_quantize_kv(keys, values, self.key_codec, self.value_codec, self.keys.indices,
-                               self.keys.norms, self.values.indices, self.values.norms,
-                               self.offset)
+        if isinstance(self.key_codec, ProdCodec):
+            self.key_codec.quantize_into(keys, self.keys, self.offset)
+            ops.append_quantize(values, self.value_codec, self.values.indices, self.values.norms,
+                                self.offset)
+        else:
+            ops.append_quantize_kv(keys, values, self.key_codec, self.value_codec, self.keys.indices,
+                                   self.keys.norms, self.values.indices, self.values.norms,
+                                   self.offset)
         self.offset = new_end
         ks, vs = self.state
         return (
@@ -289,13 +309,19 @@ class TurboQuantKVCache(_BaseCache):
         """f32 reconstructions (B, H, T, D) (turboquant_cache.py:5070-5077)."""
         ks, vs = self._states(keys_state, values_state)
         self._ensure_codecs_from_meta()
-        return (ops.dequantize(ks.indices, ks.norms, self.key_codec),
-                ops.dequantize(vs.indices, vs.norms, self.value_codec))
+        if isinstance(self.key_codec, ProdCodec):
+            k = self.key_codec.dequantize(ks)
+        else:
+            k = ops.dequantize(ks.indices, ks.norms, self.key_codec)
+        return k, ops.dequantize(vs.indices, vs.norms, self.value_codec)
 
     def _attend(self, queries, keys_state, values_state, scale, mask):
         ks, vs = self._states(keys_state, values_state)
         self._ensure_codecs_from_meta()
         causal = _mask_is_causal(mask, queries.shape[-2])
+        if isinstance(self.key_codec, ProdCodec):
+            return attention_prod(queries, ks, vs.norms, vs.indices, self.key_codec,
+                                  self.value_codec, scale, causal)
         return ops.attention_packed(queries, ks.norms, ks.indices, vs.norms, vs.indices,
                                     self.key_codec, self.value_codec, scale, causal)
 
@@ -335,7 +361,7 @@ class TurboQuantKVCache(_BaseCache):
         if self.keys is None:
             return []
         o = self.offset
-        return (TurboQuantMSEState(self.keys.norms[..., :o], self.keys.indices[..., :o, :]),
+        return (type(self.keys)(*(t[:, :, :o] for t in self.keys)),
                 TurboQuantMSEState(self.values.norms[..., :o], self.values.indices[..., :o, :]))
 
     @state.setter
@@ -348,9 +374,12 @@ class TurboQuantKVCache(_BaseCache):
             value = (value.get("keys"), value.get("values"))
         if isinstance(value, (list, tuple)) and len(value) == 2:
             k, v = value
-            self.keys = TurboQuantMSEState(*k) if not isinstance(k, TurboQuantMSEState) else k
+            if not isinstance(k, (TurboQuantMSEState, TurboQuantProdState)):
+                k = TurboQuantProdState(*k) if len(k) == 4 else TurboQuantMSEState(*k)
+            if isinstance(k, TurboQuantProdState):
+                self.key_quantizer = "prod"
             self.values = TurboQuantMSEState(*v) if not isinstance(v, TurboQuantMSEState) else v
-            self.keys = TurboQuantMSEState(self.keys.norms.contiguous(), self.keys.indices.contiguous())
+            self.keys = type(k)(*(t.contiguous() for t in k))
             self.values = TurboQuantMSEState(self.values.norms.contiguous(),
                                              self.values.indices.contiguous())
             self.offset = self.keys.norms.shape[2]
@@ -363,7 +392,10 @@ class TurboQuantKVCache(_BaseCache):
         """(offset, bits, seed, k_dim, v_dim) as strings (turboquant_cache.py:6046-6050)."""
         k_dim = self.key_codec.dim if self.key_codec else self._dims[0]
         v_dim = self.value_codec.dim if self.value_codec else self._dims[1]
-        return tuple(map(str, (self.offset, self.bits, self.seed, k_dim, v_dim)))
+        fields = (self.offset, self.bits, self.seed, k_dim, v_dim)
+        if self.key_quantizer == "prod":  # an extra field only for Prod keys
+            fields += ("prod",)
+        return tuple(map(str, fields))
 
     @meta_state.setter
     def meta_state(self, value):
@@ -372,6 +404,8 @@ class TurboQuantKVCache(_BaseCache):
         self.seed = int(float(value[2]))
         if len(value) >= 5:
             self._dims = (int(float(value[3])), int(float(value[4])))
+        if len(value) >= 6:
+            self.key_quantizer = value[5]
 
     def is_trimmable(self):
         return True
@@ -668,7 +702,8 @@ def load_prompt_cache(file_name: str, return_metadata: bool = False, device=None
         if cls_name == "TurboQuantKVCache":
             cls = TurboQuantKVCache
             if isinstance(st, list) and len(st) == 2 and all(isinstance(s, list) for s in st):
-                st = (TurboQuantMSEState(*st[0]), TurboQuantMSEState(*st[1]))
+                kst = TurboQuantProdState(*st[0]) if len(st[0]) == 4 else TurboQuantMSEState(*st[0])
+                st = (kst, TurboQuantMSEState(*st[1]))
             else:
                 st = []
         elif cls_name in ("BatchTurboQuantKVCache", "BatchKVCache"):

@@ -145,3 +145,21 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises(ValueError, match="Hadamard"):
         ops.Codec(96, 3, 0, rotation="hadamard")
     assert ops.Codec(96, 3, 0).rotation == "dense"
+
+
+def test_prod_key_quantizer_options_and_meta_state():
+    c = TurboQuantKVCache(bits=3, key_quantizer="prod")
+    assert c.key_quantizer == "prod"
+    with pytest.raises(ValueError):
+        TurboQuantKVCache(bits=3, key_quantizer="qjl")
+    with pytest.raises(ValueError):
+        TurboQuantKVCache(bits=3, key_quantizer="prod", rotation="dense")
+    # meta_state gains a sixth field only for Prod keys, and a CPU state round trip keeps it
+    assert len(TurboQuantKVCache(bits=3).meta_state) == 5
+    from kaplumba_amd.prod import TurboQuantProdState
+    st = (TurboQuantProdState(torch.ones(1, 2, 7), torch.zeros(1, 2, 7, 8, dtype=torch.uint32),
+                              torch.ones(1, 2, 7), torch.zeros(1, 2, 7, 4, dtype=torch.uint32)),
+          TurboQuantMSEState(torch.ones(1, 2, 7), torch.zeros(1, 2, 7, 12, dtype=torch.uint32)))
+    c2 = TurboQuantKVCache.from_state(st, ("7", "3.0", "0", "128", "128", "prod"))
+    assert c2.key_quantizer == "prod" and c2.offset == 7 and c2.meta_state[5] == "prod"
+    assert isinstance(c2.state[0], TurboQuantProdState) and c2.nbytes > 0

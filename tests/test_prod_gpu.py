@@ -179,3 +179,52 @@ def test_prod_left_padded_rows(device):
 def test_prod_rejects_unbuilt_shapes(device):
     with pytest.raises(NotImplementedError):
         _prod_case(device, 9, 1, 32, 8, 4, 300, 128, 3, 3)   # 16 rows per kv head
+
+
+def test_cache_with_prod_keys_decode_and_save_load(device, tmp_path):
+    """TurboQuantKVCache(key_quantizer="prod"): append, decode through the
+    model-layer dispatch, dequantize, and a save / load round trip."""
+    import math
+
+    from kaplumba_amd import (TurboQuantKVCache, load_prompt_cache, save_prompt_cache,
+                              scaled_dot_product_attention)
+    from kaplumba_amd.prod import TurboQuantProdState
+    from tests import test_attention_gpu as _A
+
+    B, Hq, Hkv, D = 1, 8, 2, 128
+    g = torch.Generator().manual_seed(5)
+    cache = TurboQuantKVCache(bits=3.5, key_quantizer="prod")   # keys: Prod 3 bits, values: MSE 4
+    ks = [torch.randn(B, Hkv, 300, D, generator=g).to(torch.bfloat16)]
+    vs = [torch.randn(B, Hkv, 300, D, generator=g).to(torch.bfloat16)]
+    kst, vst = cache.update_and_fetch(ks[0].to(device), vs[0].to(device))
+    for _ in range(3):
+        ks.append(torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16))
+        vs.append(torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16))
+        kst, vst = cache.update_and_fetch(ks[-1].to(device), vs[-1].to(device))
+    assert cache.offset == 303 and isinstance(cache.state[0], TurboQuantProdState)
+    assert cache.meta_state[5] == "prod" and cache.key_codec.bits == 3 and cache.value_codec.bits == 4
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    out = scaled_dot_product_attention(q.to(device), kst, vst, cache, 1 / math.sqrt(D), None)
+    k_all = torch.cat(ks, dim=2).float().numpy()
+    n, mse, rn, sg, _ = O.quantize_prod(k_all, 3, O.rht_signs(D, 0), O.beta_codebook(D, 2),
+                                        O.projection_matrix(D, 1))
+    st = cache.state
+    assert np.array_equal(st[0].mse_indices.cpu().numpy().astype(np.uint32), mse)
+    v_np = torch.cat(vs, dim=2).float().numpy()
+    vp, vn = O.quantize_rht(v_np, 4, O.rht_signs(D, 1), O.beta_codebook(D, 4))
+    want = O.attention_prod(q.float().numpy(), st[0].norms.cpu().numpy(),
+                            st[0].mse_indices.cpu().numpy().astype(np.uint32),
+                            st[0].residual_norms.cpu().numpy(),
+                            st[0].qjl_signs.cpu().numpy().astype(np.uint32), vp, vn, k_bits=3,
+                            v_bits=4, k_signs_rot=O.rht_signs(D, 0), k_mse_codebook=O.beta_codebook(D, 2),
+                            proj=O.projection_matrix(D, 1), v_codebook=O.beta_codebook(D, 4),
+                            v_rot=O.rht_signs(D, 1), scale=1 / math.sqrt(D), q_dtype="bf16")
+    _A.assert_close(out, want, "bf16", "prod cache decode")
+    kd, vd = cache.dequantize()
+    assert kd.shape == (B, Hkv, 303, D) and vd.shape == (B, Hkv, 303, D)
+    f = str(tmp_path / "prod.safetensors")
+    save_prompt_cache(f, [cache])
+    loaded = load_prompt_cache(f)[0]
+    assert loaded.key_quantizer == "prod" and isinstance(loaded.state[0], TurboQuantProdState)
+    out2 = loaded.decode_attention(q.to(device), scale=1 / math.sqrt(D))
+    assert torch.equal(out, out2)
