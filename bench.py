@@ -279,15 +279,16 @@ def bench_prefill_append(torch, args, dev):
     qbytes = quantize_bytes(H * T, D, bits, 2, 4)           # one K or V launch
     pbytes = H * T * D * 2 * 2                              # plain layer tensor: read + write
     total = n_q * 2 * qbytes + c["plain_layers"] * 2 * pbytes
-    launch_us = ms_q * 1e3 / (2 * n_q)
-    flops = 2.0 * H * T * D * D                             # u @ R^T per launch
+    launch_us = ms_q * 1e3 / (2 * n_q)                      # per K or V tensor (half a K+V launch)
+    flops = 2.0 * H * T * D * D                             # u @ R^T per tensor
     return {"workload": "cfg3 prefill append: 36 layers x bf16 K,V [8,8192,128]; layers 0-3 stored "
                         "unquantized, 4-35 dense 128x128 rotation (matrix cores) + 3-bit pack, f32 norms",
             "value": round(total / (ms * 1e-3) / 1e9, 2), "unit": "GB/s",
             "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "us_per_step": round(ms * 1e3, 2), "bytes_per_step": total,
             "prefill_tokens_per_s": round(T * 1e3 / ms, 1),
-            "dense_quantize": {"us_per_launch": round(launch_us, 3), "bytes_per_launch": qbytes,
+            "dense_quantize": {"us_per_tensor": round(launch_us, 3), "bytes_per_tensor": qbytes,
+                               "launches": "one append_dense_kv_kernel per layer (K and V)",
                                "GB/s": round(qbytes / (launch_us * 1e-6) / 1e9, 2),
                                "rotation_tflops": round(flops / (launch_us * 1e-6) / 1e12, 1),
                                "mfma_frac": round(3 * flops / (launch_us * 1e-6) / 1e12

@@ -82,10 +82,10 @@ int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
  * _write_state) in one call.  Each side is exactly tq_append_quantize with
  * its own x, strides, bits, rotation vector / matrix, midpoints and
  * destination; the shape (B, H, L, dim), x_dtype, rot_kind, norm_dtype,
- * capacity and offset are shared.  The Hadamard rotation with F16 / BF16
- * input at dim 64 / 128 / 256 and equal widths or v_bits = k_bits + 1 (the
- * x.5-bit split) runs both sides in one kernel launch; other cases run the
- * two quantizers one after the other.  Results are identical either way.
+ * capacity and offset are shared.  F16 / BF16 input at dim 64 / 128 / 256
+ * with equal widths or v_bits = k_bits + 1 (the x.5-bit split) runs both
+ * sides in one kernel launch, for either rotation; other cases run the two
+ * quantizers one after the other.  Results are identical either way.
  */
 int tq_append_quantize_kv(const void* k_x, const void* v_x, int x_dtype, int B, int H, int L,
                           int dim, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_l,

@@ -20,6 +20,10 @@ struct AppendArgs {
 
 // Dense-rotation quantizer on the matrix cores (tq_append_dense.hip).
 int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
+// Keys and values in one launch (16-bit input, dim 64 / 128 / 256, equal
+// widths or v_bits = k_bits + 1); returns -1 for other cases.
+int launch_append_dense_kv(const AppendArgs& k, const AppendArgs& v, int dim, int kbits, int vbits,
+                           int x_dtype, hipStream_t st);
 // The same product for f32 input with a one-bit output (x @ R^T >= 0), the
 // Prod codec's QJL signs; norms receive ||x||.
 int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st);

@@ -444,6 +444,10 @@ extern "C" int tq_append_quantize_kv(const void* k_x, const void* v_x, int x_dty
                     v_midpoints, v_packed, v_norms, norm_dtype, capacity, offset, va, &empty);
   if (rc || empty) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rot_kind == TQ_ROT_DENSE) {
+    rc = launch_append_dense_kv(ka, va, dim, k_bits, v_bits, x_dtype, st);
+    if (rc != -1) return rc;
+  }
   if (rot_kind == TQ_ROT_HADAMARD) {
     switch (dim) {
       case 64: rc = launch_kv_dtype<64>(x_dtype, k_bits, v_bits, ka, va, st); break;

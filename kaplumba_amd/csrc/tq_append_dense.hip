@@ -70,14 +70,20 @@ __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Split f into NP bf16 pieces (round-to-nearest-even each, exact remainders).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Split a and b into NP bf16 pieces each (round-to-nearest-even, exact
+// remainders), packed per piece as (a_i, b_i): one v_cvt_pk_bf16_f32 per piece
+// and pair.
 template <int NP>
-__device__ __forceinline__ void split_bf16(float f, uint16_t (&p)[NP]) {
-  float r = f;
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t (&w)[NP]) {
+  float ra = a, rb = b;
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
-    p[i] = f32_to_bf16_bits(r);
-    r = __fsub_rn(r, bf16_bits_to_f32(p[i]));
+    const bf16x2_t v = {static_cast<__bf16>(ra), static_cast<__bf16>(rb)};
+    w[i] = __builtin_bit_cast(uint32_t, v);
+    ra = __fsub_rn(ra, __uint_as_float(w[i] << 16));
+    rb = __fsub_rn(rb, __uint_as_float(w[i] & 0xffff0000u));
   }
 }
 
@@ -95,23 +101,24 @@ __device__ __forceinline__ float x_elem(const u32x4_t (&xr)[NX], int e) {
 
 // GE: one-bit signs of x @ R^T, bit = (y >= 0) (the QJL sketch of the Prod
 // codec, turboquant_cache.py:4662-4663); midpoints are not read.
-template <int D, int BITS, int XDT, bool GE = false>
-__global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs a) {
+// Workgroup bid of nblk (persistent over vector tiles) of one quantize side;
+// s_r: the workgroup's LDS for the R pieces (S::SLOTS fragments).
+template <int D, int BITS, int XDT, bool GE>
+__device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, int bid, int nblk) {
   using S = DenseShape<D>;
   using XP = XPieces<XDT>;
   constexpr int NMID = (1 << BITS) - 1;
   constexpr int PW = D * BITS / 32;
   constexpr int NX = S::LE * XP::ES / 16;  // 16-byte loads per lane
-  __shared__ u32x4_t s_r[S::SLOTS];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
   const int vl = lane % 32;
   const int g = lane / 32;
-  const int slice = blockIdx.x % S::NSLICE;
+  const int slice = bid % S::NSLICE;
   const int c0 = slice * S::CT;
-  const int64_t tile_stride = gridDim.x / S::NSLICE;
+  const int64_t tile_stride = nblk / S::NSLICE;
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
 
   // Input run of this lane for a given tile (zeros past the last vector).
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
     }
   };
 
-  int64_t tile = blockIdx.x / S::NSLICE;
+  int64_t tile = bid / S::NSLICE;
   u32x4_t xr[NX];
   int64_t row;
   load_x(tile, xr, row);  // in flight while R is split into LDS
@@ -154,11 +161,10 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
     uint32_t w[S::NRP][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint16_t lo[S::NRP], hi[S::NRP];
-      split_bf16<S::NRP>(e[2 * j], lo);
-      split_bf16<S::NRP>(e[2 * j + 1], hi);
+      uint32_t pr[S::NRP];
+      split_bf16x2<S::NRP>(e[2 * j], e[2 * j + 1], pr);
 #pragma unroll
-      for (int p = 0; p < S::NRP; ++p) w[p][j] = lo[p] | (static_cast<uint32_t>(hi[p]) << 16);
+      for (int p = 0; p < S::NRP; ++p) w[p][j] = pr[p];
     }
 #pragma unroll
     for (int p = 0; p < S::NRP; ++p)
@@ -211,14 +217,13 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
       if constexpr (XDT == TQ_DTYPE_BF16) {
         xb[0] = xr[ks];
       } else {
-        uint16_t pc[8][XP::N];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) split_bf16<XP::N>(x_elem<XDT, NX>(xr, 8 * ks + j), pc[j]);
+        for (int j = 0; j < 4; ++j) {
+          uint32_t pr[XP::N];
+          split_bf16x2<XP::N>(x_elem<XDT, NX>(xr, 8 * ks + 2 * j), x_elem<XDT, NX>(xr, 8 * ks + 2 * j + 1), pr);
 #pragma unroll
-        for (int p = 0; p < XP::N; ++p)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            xb[p][j] = pc[2 * j][p] | (static_cast<uint32_t>(pc[2 * j + 1][p]) << 16);
+          for (int p = 0; p < XP::N; ++p) xb[p][j] = pr[p];
+        }
       }
       // smallest terms first
 #pragma unroll
@@ -271,6 +276,24 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
   }
 }
 
+template <int D, int BITS, int XDT, bool GE = false>
+__global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs a) {
+  __shared__ u32x4_t s_r[DenseShape<D>::SLOTS];
+  dense_body<D, BITS, XDT, GE>(a, s_r, blockIdx.x, gridDim.x);
+}
+
+// Keys and values of one append in one launch: workgroups below nk quantize
+// the keys (R_K), the rest the values (R_V); each splits its side's R once and
+// walks that side's tiles, sharing one LDS buffer between the two bodies.
+template <int D, int KBITS, int VBITS, int XDT>
+__global__ __launch_bounds__(kDenseThreads) void append_dense_kv_kernel(AppendArgs k, AppendArgs v, int nk) {
+  __shared__ u32x4_t s_r[DenseShape<D>::SLOTS];
+  if (static_cast<int>(blockIdx.x) < nk)
+    dense_body<D, KBITS, XDT, false>(k, s_r, blockIdx.x, nk);
+  else
+    dense_body<D, VBITS, XDT, false>(v, s_r, blockIdx.x - nk, gridDim.x - nk);
+}
+
 template <int D, int BITS>
 int launch_dense_bits(const AppendArgs& a, int x_dtype, hipStream_t st) {
   using S = DenseShape<D>;
@@ -315,7 +338,54 @@ int launch_dense_signs_dim(const AppendArgs& a, hipStream_t st) {
   return check_launch("append_dense_kernel (signs)");
 }
 
+template <int D, int KBITS, int VBITS, int XDT>
+int launch_dense_kv_pair(const AppendArgs& k, const AppendArgs& v, hipStream_t st) {
+  using S = DenseShape<D>;
+  const int64_t n_vec = static_cast<int64_t>(k.B) * k.H * k.L;
+  const int64_t tiles = (n_vec + S::VPT - 1) / S::VPT;
+  // half the CUs per side, one workgroup each (the R pieces fill the LDS)
+  const int64_t per_slice = std::min<int64_t>(tiles, std::max(1, device_cu_count() / S::NSLICE / 2));
+  const int nk = static_cast<int>(per_slice * S::NSLICE);
+  hipLaunchKernelGGL((append_dense_kv_kernel<D, KBITS, VBITS, XDT>), dim3(static_cast<unsigned>(2 * nk)),
+                     dim3(kDenseThreads), 0, st, k, v, nk);
+  return check_launch("append_dense_kv_kernel");
+}
+
+template <int D, int XDT>
+int launch_dense_kv_bits(int kbits, int vbits, const AppendArgs& k, const AppendArgs& v, hipStream_t st) {
+  switch (kbits * 8 + vbits) {
+    case 1 * 8 + 1: return launch_dense_kv_pair<D, 1, 1, XDT>(k, v, st);
+    case 2 * 8 + 2: return launch_dense_kv_pair<D, 2, 2, XDT>(k, v, st);
+    case 3 * 8 + 3: return launch_dense_kv_pair<D, 3, 3, XDT>(k, v, st);
+    case 4 * 8 + 4: return launch_dense_kv_pair<D, 4, 4, XDT>(k, v, st);
+    case 1 * 8 + 2: return launch_dense_kv_pair<D, 1, 2, XDT>(k, v, st);
+    case 2 * 8 + 3: return launch_dense_kv_pair<D, 2, 3, XDT>(k, v, st);
+    case 3 * 8 + 4: return launch_dense_kv_pair<D, 3, 4, XDT>(k, v, st);
+  }
+  return -1;
+}
+
+template <int D>
+int launch_dense_kv_dim(int x_dtype, int kbits, int vbits, const AppendArgs& k, const AppendArgs& v,
+                        hipStream_t st) {
+  if (x_dtype == TQ_DTYPE_F16) return launch_dense_kv_bits<D, TQ_DTYPE_F16>(kbits, vbits, k, v, st);
+  if (x_dtype == TQ_DTYPE_BF16) return launch_dense_kv_bits<D, TQ_DTYPE_BF16>(kbits, vbits, k, v, st);
+  return -1;
+}
+
 }  // namespace
+
+int launch_append_dense_kv(const AppendArgs& k, const AppendArgs& v, int dim, int kbits, int vbits,
+                           int x_dtype, hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(k.rot) & 15u) != 0 || (reinterpret_cast<uintptr_t>(v.rot) & 15u) != 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append: dense rotation matrix must be 16-byte aligned");
+  switch (dim) {
+    case 64: return launch_dense_kv_dim<64>(x_dtype, kbits, vbits, k, v, st);
+    case 128: return launch_dense_kv_dim<128>(x_dtype, kbits, vbits, k, v, st);
+    case 256: return launch_dense_kv_dim<256>(x_dtype, kbits, vbits, k, v, st);
+  }
+  return -1;
+}
 
 int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st) {
   if ((reinterpret_cast<uintptr_t>(a.rot) & 15u) != 0)
