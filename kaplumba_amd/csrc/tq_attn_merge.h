@@ -72,32 +72,106 @@ struct RowSet {
   }
 };
 
+// Rows j < nrows of y (LDS, [NQ][D] f32) through the dense R_V^-1:
+// x[j][d] = scl(j) * sum_k y[j][k] R_V[k][d], stored as output row qoff(j).
+// One pass over R_V (D x D f32, row-major, read from L2 once per workgroup):
+// thread (column group c, k slice ks) owns four columns of every row over
+// D / KS values of k and streams its R_V rows as float4, up to 32 loads in
+// flight (the read is latency-bound: few round trips matter more than
+// instruction count).  The y reads are LDS broadcasts.  The slices are added
+// through s_part ([NT / 64][NQ][D] f32 of LDS, not aliasing y).  Rows past
+// nrows are summed too (uniform work, never stored).  All threads call it.
+template <int D, int NQ, int NT, class Off, class Scale>
+__device__ __forceinline__ void dense_rows_out(const AttnParams& p, const float* y, float* s_part,
+                                               int nrows, Off qoff, Scale scl) {
+  constexpr int C4 = D / 4;
+  constexpr int NW = NT / kWave;
+  constexpr int KS = NT / C4 < NW ? NT / C4 : NW;  // k slices (s_part holds NW)
+  constexpr int KR = D / KS;                        // k values per slice
+  constexpr int KU = KR < 32 ? KR : 32;             // loads in flight
+  static_assert(KS >= 1 && D % KS == 0 && KR % KU == 0 && KU % 4 == 0, "dense rows mapping");
+  const int c = threadIdx.x % C4;
+  const int ks = threadIdx.x / C4;
+  if (ks < KS) {
+    float4 acc[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4* r4 = reinterpret_cast<const float4*>(p.vrot) + c;
+    const float4* y4 = reinterpret_cast<const float4*>(y);
+#pragma unroll 1
+    for (int k0 = ks * KR; k0 < (ks + 1) * KR; k0 += KU) {
+      float4 r[KU];
+#pragma unroll
+      for (int u = 0; u < KU; ++u) r[u] = r4[(k0 + u) * C4];
+#pragma unroll
+      for (int j = 0; j < NQ; ++j)
+#pragma unroll
+        for (int u4 = 0; u4 < KU / 4; ++u4) {
+          const float4 yv = y4[(j * D + k0) / 4 + u4];
+          const float ys[4] = {yv.x, yv.y, yv.z, yv.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float4 rv = r[4 * u4 + e];
+            acc[j].x = fmaf(ys[e], rv.x, acc[j].x);
+            acc[j].y = fmaf(ys[e], rv.y, acc[j].y);
+            acc[j].z = fmaf(ys[e], rv.z, acc[j].z);
+            acc[j].w = fmaf(ys[e], rv.w, acc[j].w);
+          }
+        }
+    }
+    float4* part4 = reinterpret_cast<float4*>(s_part);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) part4[(ks * NQ + j) * C4 + c] = acc[j];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < NQ * C4; idx += NT) {
+    const int j = idx / C4;
+    const int cc = idx % C4;
+    if (j >= nrows) break;  // idx grows: every later index is past nrows too
+    const float4* part4 = reinterpret_cast<const float4*>(s_part);
+    float4 a = part4[j * C4 + cc];
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const float4 t = part4[(k * NQ + j) * C4 + cc];
+      a.x += t.x;
+      a.y += t.y;
+      a.z += t.z;
+      a.w += t.w;
+    }
+    const float s = scl(j);
+    const int64_t o = qoff(j) * D + 4 * cc;
+    store_out(p.out, p.q_dtype, o, a.x * s);
+    store_out(p.out, p.q_dtype, o + 1, a.y * s);
+    store_out(p.out, p.q_dtype, o + 2, a.z * s);
+    store_out(p.out, p.q_dtype, o + 3, a.w * s);
+  }
+}
+
 // Normalise s_o rows by 1/max(l, eps), apply R_V^-1 and store.  s_o: [NQ][D];
-// s_vsign: D floats of LDS scratch.
+// s_vsign: D floats of LDS scratch; s_part: [NT / 64][NQ][D] f32 of LDS
+// scratch for the dense rotation (unused otherwise).
 template <int D, int NQ, int NT>
 __device__ void finalize_rows(const AttnParams& p, const RowSet& rs, float* s_o,
-                              const float* s_l, float* s_vsign, bool plain, bool dense) {
+                              const float* s_l, float* s_vsign, float* s_part, bool plain, bool dense) {
   if (!plain && !dense)
     for (int d = threadIdx.x; d < D; d += NT) s_vsign[d] = p.vrot[d];
   for (int idx = threadIdx.x; idx < NQ * D; idx += NT)
     s_o[idx] = s_o[idx] / fmaxf(s_l[idx / D], kNormEps);
   __syncthreads();
-  if (!plain && !dense) lds_fwht<D, NQ, NT>(s_o);
+  if (!plain && dense) {
+    int nrows = 0;
+    while (nrows < NQ && rs.valid(nrows)) ++nrows;  // valid rows are a prefix
+    dense_rows_out<D, NQ, NT>(p, s_o, s_part, nrows, [&](int j) { return rs.qoff(j); },
+                              [](int) { return 1.f; });
+    return;
+  }
+  if (!plain) lds_fwht<D, NQ, NT>(s_o);
   for (int idx = threadIdx.x; idx < NQ * D; idx += NT) {
     const int j = idx / D;
     const int d = idx % D;
     if (!rs.valid(j)) continue;
     float r = s_o[idx];
-    if (!plain) {
-      if (!dense) {
-        r = r * p.rscale * s_vsign[d];
-      } else {
-        float a2 = 0.f;  // x_d = sum_k y_k R[k][d]
-        for (int k2 = 0; k2 < D; ++k2)
-          a2 = fmaf(s_o[j * D + k2], p.vrot[static_cast<int64_t>(k2) * D + d], a2);
-        r = a2;
-      }
-    }
+    if (!plain) r = r * p.rscale * s_vsign[d];
     store_out(p.out, p.q_dtype, rs.qoff(j) * D + d, r);
   }
 }

@@ -165,6 +165,7 @@ struct MfmaShape {
   static constexpr int ML_OFF = O_OFF + NQ * D * 4;   // [NQ][2]
   static constexpr int AUX_OFF = ML_OFF + (NQ * 8 + 15) / 16 * 16;  // [NQ + D] f32 finalize scratch
   static constexpr int POST_BYTES = AUX_OFF + (NQ + D) * 4;
+  static_assert(O_OFF % 16 == 0, "combined rows are read as float4");
   static constexpr int BYTES = LOOP_BYTES > POST_BYTES ? LOOP_BYTES : POST_BYTES;
   static constexpr int RPW = (NQ + NW - 1) / NW;  // query rows rotated per wave
   static constexpr int QPL = D / kWave;           // query elements per lane and row
@@ -820,7 +821,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   if (nvalid == 1) {  // the only split: finish here (plain = no rotation left for Hadamard)
     if (tid < NQ) s_aux[tid] = s_ml[2 * tid + 1];
     lds_barrier();
-    finalize_rows<D, NQ, NT>(p, rs, s_o, s_aux, s_aux + NQ, !dense, dense);
+    finalize_rows<D, NQ, NT>(p, rs, s_o, s_aux, s_aux + NQ, s_co, !dense, dense);  // s_co is dead
     return;
   }
   // the split's partial, merged by attn_merge_kernel after this kernel

@@ -448,7 +448,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_plain_kernel(Att
   if (nvalid == 1) {  // the only split: finish here
     if (tid < NQ) s_aux[tid] = s_ml[2 * tid + 1];
     lds_barrier();
-    finalize_rows<D, NQ, NT>(p, rs, s_o, s_aux, s_aux + NQ, true, false);
+    finalize_rows<D, NQ, NT>(p, rs, s_o, s_aux, s_aux + NQ, nullptr, true, false);
     return;
   }
   const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;

@@ -106,6 +106,7 @@ struct SmallShape {
   static constexpr int WF_OFF = WE_OFF + NW * NQ * 4;      // [NW][NQ] combine factors
   static constexpr int FO_OFF = WF_OFF + NW * NQ * 4;      // [NQ][D] final rows
   static constexpr int FL_OFF = FO_OFF + NQ * D * 4;       // [NQ] l, [NQ] m
+  static_assert(FO_OFF % 16 == 0, "final rows are read as float4");
   static constexpr int FLAG_OFF = FL_OFF + 2 * NQ * 4;
   static constexpr int POST_BYTES = FLAG_OFF + 16;
   static constexpr int BYTES = LOOP_BYTES > POST_BYTES ? LOOP_BYTES : POST_BYTES;
@@ -796,16 +797,10 @@ __global__ __launch_bounds__(512, 1) void attn_small_kernel(AttnParams p) {
         store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * p.vrot[lane + e * kWave]);
     }
   } else {
-    for (int idx = tid; idx < NQ * D; idx += NT) {
-      const int r = idx / D;
-      const int c = idx % D;
-      if (r >= nrows) continue;
+    dense_rows_out<D, NQ, NT>(p, s_fo, s_wo, nrows, row_qoff, [&](int r) {  // s_wo is dead
       const float lt = s_fl[r];
-      const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      float a2 = 0.f;  // x_c = sum_k y_k R[k][c]
-      for (int k2 = 0; k2 < D; ++k2) a2 = fmaf(s_fo[r * D + k2], p.vrot[static_cast<int64_t>(k2) * D + c], a2);
-      store_out(p.out, p.q_dtype, row_qoff(r) * D + c, a2 * inv);
-    }
+      return lt > 0.f ? 1.f / lt : 0.f;
+    });
   }
 }
 

@@ -141,6 +141,26 @@ def test_gqa_groups_and_verify_rows(device, Hq, Hkv, L):
     run_case(device, Hq * 7 + Hkv + L, 1, Hq, Hkv, L, 1500, 128, 3, 3)
 
 
+@pytest.mark.parametrize("Hq,Hkv,L,d,kb,vb,rot", [
+    (16, 8, 1, 256, 4, 2, "dense"),     # d = 256, 4-row groups, dense rotation
+    (8, 4, 2, 256, 2, 3, "hadamard"),   # d = 256, causal verify rows
+    (32, 2, 1, 64, 3, 3, "hadamard"),   # 16-row groups at d = 64
+])
+@pytest.mark.parametrize("shape", ["extreme", "tiny"])
+def test_ragged_lengths_general_kernel(device, Hq, Hkv, L, d, kb, vb, rot, shape):
+    # The general kernel over very uneven sequence lengths: empty sequences
+    # (zero rows), sequences shorter than one 32-token sub-chunk, lengths on
+    # and next to sub-chunk and split boundaries, and (tiny) a batch whose
+    # whole cache is a few tokens.
+    if shape == "extreme":
+        lens = [0, 1, 31, 32, 33, 3000, 17, 2999, 64, 1500, 0, 2048]
+        T = 3000
+    else:
+        lens = [1, 0, 2, 3, 1, 0, 2, 1]
+        T = 3
+    run_case(device, 11 + d + L, len(lens), Hq, Hkv, L, T, d, kb, vb, rot=rot, lengths=lens)
+
+
 @pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 2048, 5000])
 def test_token_counts(device, T):
     run_case(device, T, 1, 8, 2, 1, T, 128, 3, 3)
