@@ -11,37 +11,38 @@ namespace tq {
 // Dense rotation only:
 //   q_s = round_qdtype(q * scale_q)     (MLX weak-scalar multiply, :5802)
 //   q_rot = q_s @ R_K^T                 (turboquant_cache.py:4144)
-// Block (row block, coordinate block) computes q_rot[r][i] for kQprepRows
-// query rows and 64 coordinates i.  Thread (i, quarter jq) holds the quarter
-// jq of row i of R_K in registers and forms partial dot products with every
-// query row of the block (the rows are LDS broadcasts: a wave shares jq);
-// the four partials of (r, i) fold through LDS.  R_K crosses L2 once per
-// kQprepRows query rows.
-constexpr int kQprepRows = 16;
+// Block (row block, coordinate block) computes q_rot[r][i] for QR query rows
+// and 64 coordinates i.  Thread (i, quarter jq) holds the quarter jq of row
+// i of R_K in registers and forms partial dot products with every query row
+// of the block (the rows are LDS broadcasts: a wave shares jq); the four
+// partials of (r, i) fold through LDS.  R_K crosses L2 once per QR query
+// rows.  The launch is latency-bound (a few query rows per kv head), so QR is
+// the largest of 16, 8, 4 that still gives one workgroup per CU.
 constexpr int kQprepThreads = 256;
 
-template <int QDT, int D>
+template <int QDT, int D, int QR>
 __global__ __launch_bounds__(kQprepThreads) void qprep_kernel(AttnParams p, int64_t n_rows) {
   constexpr int JL = D / 4;  // coordinates j per thread
-  __shared__ float4 s_q4[kQprepRows][D / 4];
-  __shared__ float s_part[4][kQprepRows][64];
+  __shared__ float4 s_q4[QR][D / 4];
+  __shared__ float s_part[4][QR][64];
   const int tid = threadIdx.x;
   const int il = tid % 64;
   const int jq = tid / 64;
   const int i = blockIdx.y * 64 + il;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kQprepRows;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * QR;
   float4 rv[JL / 4];
   const float4* src = reinterpret_cast<const float4*>(p.krot + static_cast<int64_t>(i) * D + jq * JL);
 #pragma unroll
   for (int m = 0; m < JL / 4; ++m) rv[m] = src[m];
-  // query rows: thread (row r, segment) loads D/16 consecutive elements with
+  // query rows: thread (row r, segment) loads SEG consecutive elements with
   // independent loads (one index computation per thread)
-  static_assert(kQprepThreads == 16 * kQprepRows, "one segment per thread");
+  static_assert(kQprepThreads % QR == 0 && D * QR % kQprepThreads == 0, "one segment per thread");
   {
-    constexpr int SEG = D / 16;
+    constexpr int TPR = kQprepThreads / QR;  // threads per row
+    constexpr int SEG = D / TPR;
     float* s_q = reinterpret_cast<float*>(s_q4);
-    const int r = tid / 16;
-    const int j0 = (tid % 16) * SEG;
+    const int r = tid / TPR;
+    const int j0 = (tid % TPR) * SEG;
     const int64_t row = row0 + r;  // (b*Hq + h)*L + l
     float v[SEG];
     if (row < n_rows) {
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(kQprepThreads) void qprep_kernel(AttnParams p, int6
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kQprepRows; ++r) {
+  for (int r = 0; r < QR; ++r) {
     float acc = 0.f;
 #pragma unroll
     for (int m = 0; m < JL / 4; ++m) {
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(kQprepThreads) void qprep_kernel(AttnParams p, int6
     s_part[jq][r][il] = acc;
   }
   __syncthreads();
-  for (int o = tid; o < kQprepRows * 64; o += kQprepThreads) {
+  for (int o = tid; o < QR * 64; o += kQprepThreads) {
     const int r = o / 64;
     const int c = o % 64;
     if (row0 + r < n_rows)
@@ -85,14 +86,26 @@ __global__ __launch_bounds__(kQprepThreads) void qprep_kernel(AttnParams p, int6
   }
 }
 
+template <int D, int QR>
+void launch_qprep_qr(const AttnParams& p, int q_dtype, int64_t rows, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((rows + QR - 1) / QR), D / 64);
+  switch (q_dtype) {
+    case TQ_DTYPE_F32: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_F32, D, QR>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
+    case TQ_DTYPE_F16: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_F16, D, QR>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
+    default: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_BF16, D, QR>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
+  }
+}
+
 template <int D>
 void launch_qprep(const AttnParams& p, int q_dtype, int64_t rows, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((rows + kQprepRows - 1) / kQprepRows), D / 64);
-  switch (q_dtype) {
-    case TQ_DTYPE_F32: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_F32, D>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
-    case TQ_DTYPE_F16: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_F16, D>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
-    default: hipLaunchKernelGGL((qprep_kernel<TQ_DTYPE_BF16, D>), grid, dim3(kQprepThreads), 0, st, p, rows); break;
-  }
+  const int64_t blocks16 = (rows + 15) / 16 * (D / 64);
+  const int64_t cus = device_cu_count();
+  if (blocks16 >= cus)
+    launch_qprep_qr<D, 16>(p, q_dtype, rows, st);
+  else if (2 * blocks16 >= cus)
+    launch_qprep_qr<D, 8>(p, q_dtype, rows, st);
+  else
+    launch_qprep_qr<D, 4>(p, q_dtype, rows, st);
 }
 
 // ------------------------------------------------------------- planning ---

@@ -487,29 +487,30 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   const float sk = f16_split_scale(kmax);
   const float cbs_v = f16_split_scale(vmax);
   {
-    // Thread t computes the entry of key t % KEYS once and stores it in the
-    // replicas (s + key) % REP for its slots s = t / KEYS, t / KEYS + NT / KEYS,
+    // Thread t computes the entry of key t % K once (K = min(KEYS, NT);
+    // keys t, t + NT, ... when there are more keys than threads) and stores
+    // it in the replicas (s + key) % REP for its slots s = t / K, t / K + NT / K,
     // ...: rotating the replica by the key keeps the lanes of one store on
     // distinct banks (key-major addresses alone would put them all on one).
-    static_assert(NT % S::KKEYS == 0 && NT % S::VKEYS == 0, "table build mapping");
+    constexpr int KK = S::KKEYS < NT ? S::KKEYS : NT;
+    constexpr int VK = S::VKEYS < NT ? S::VKEYS : NT;
+    static_assert(NT % KK == 0 && NT % VK == 0, "table build mapping");
     uint2* lk = reinterpret_cast<uint2*>(lds + S::LUTK_OFF);
-    {
-      const int key = tid % S::KKEYS;
+    for (int key = tid % KK; key < S::KKEYS; key += KK) {
       uint32_t h0, l0, h1, l1;
       split_f16(ckb[key & ((1 << KB) - 1)] * sk, h0, l0);
       split_f16(ckb[key >> KB] * sk, h1, l1);
       const uint2 ent = make_uint2(h0 | (h1 << 16), l0 | (l1 << 16));
-      for (int sl = tid / S::KKEYS; sl < REPK; sl += NT / S::KKEYS)
+      for (int sl = tid / KK; sl < REPK; sl += NT / KK)
         lk[key * REPK + (sl + key) % REPK] = ent;
     }
     uint2* lv = reinterpret_cast<uint2*>(lds + S::LUTV_OFF);
-    {
-      const int key = tid % S::VKEYS;
+    for (int key = tid % VK; key < S::VKEYS; key += VK) {
       uint32_t h0, l0, h1, l1;
       split_f16(cvb[key & ((1 << VB) - 1)] * cbs_v, h0, l0);
       split_f16(cvb[key >> VB] * cbs_v, h1, l1);
       const uint2 ent = make_uint2(h0 | (h1 << 16), l0 | (l1 << 16));
-      for (int sl = tid / S::VKEYS; sl < REPV; sl += NT / S::VKEYS)
+      for (int sl = tid / VK; sl < REPV; sl += NT / VK)
         lv[key * REPV + (sl + key) % REPV] = ent;
     }
   }
