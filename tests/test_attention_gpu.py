@@ -183,6 +183,7 @@ def test_ragged_batch_dense_d256(device):
     (128, 32, 8, 4, 2500),   # 16-row groups (GQA 4 x 4 drafts), causal
     (128, 8, 8, 1, 700),     # MHA, one row per group
     (256, 8, 2, 3, 2100),    # three 4-row groups per kv head, causal
+    (128, 32, 8, 32, 300),   # 2,048 query rows: the query rotation's 16-row blocks
 ])
 def test_dense_rotation_shapes(device, d, Hq, Hkv, L, T):
     """Dense R_K / R_V: the query rotation and the merge's R_V^-1 over whole row groups."""
