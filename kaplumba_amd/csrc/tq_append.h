@@ -18,6 +18,37 @@ struct AppendArgs {
   float scale;         // f32(1/sqrt(D)), Hadamard only
 };
 
+// u[i] = x[i] / den with IEEE (correctly rounded) division, den = max(n, 1e-6)
+// the vector's norm.  The quotient comes from the correctly rounded
+// reciprocal r = RN(1 / den), one division per vector: q = RN(x r) is within
+// an ulp of x / den, the residual e = x - q den is exact in one fma, and
+// RN(q + e r) is the correctly rounded quotient (Markstein's theorem) while
+// quotient and residual stay clear of the subnormal range.  That holds for
+// every f16 input (|x| >= 2^-24 or 0, den < 2^21); bf16 and f32 inputs take
+// the division itself when an element is below 2^-100 in magnitude (zeros
+// aside: a zero quotient may differ only in its sign, which no index or sum
+// sees) or den is not below 2^100.  x and u may be the same array.
+template <int XDT>
+__device__ __forceinline__ void div_by_norm(const float (&x)[32], float den, float (&u)[32]) {
+  bool slow = false;
+  if constexpr (XDT != TQ_DTYPE_F16) {
+    slow = !(den < 0x1p100f);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) slow |= x[i] != 0.f && fabsf(x[i]) < 0x1p-100f;
+  }
+  if (slow) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) u[i] = __fdiv_rn(x[i], den);
+  } else {
+    const float r = __fdiv_rn(1.f, den);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float q = __fmul_rn(x[i], r);
+      u[i] = __builtin_fmaf(__builtin_fmaf(-q, den, x[i]), r, q);
+    }
+  }
+}
+
 // Dense-rotation quantizer on the matrix cores (tq_append_dense.hip).
 int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
 // Keys and values in one launch (16-bit input, dim 64 / 128 / 256, equal

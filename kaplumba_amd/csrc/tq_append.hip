@@ -115,9 +115,11 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   const float n = sqrt_rn(ss);
   const float den = fmaxf(n, kNormEps);
 
-  // ---- normalise and apply signs (multiplying by +-1 is exact)
+  // ---- normalise (IEEE x / den, div_by_norm) and apply signs (multiplying
+  // by +-1 is exact)
+  div_by_norm<XDT>(v, den, v);
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], den), s_sign[g * 32 + i]);
+  for (int i = 0; i < 32; ++i) v[i] = __fmul_rn(v[i], s_sign[g * 32 + i]);
 
   // ---- Walsh-Hadamard: in-lane stages (distance 1..16)
 #pragma unroll

@@ -131,8 +131,7 @@ __global__ __launch_bounds__(256) void prod_residual_kernel(ProdArgs a) {
   const float n = sqrt_rn(ss);
   const float den = fmaxf(n, kNormEps);
   float u[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) u[i] = __fdiv_rn(v[i], den);
+  div_by_norm<XDT>(v, den, u);
 
   const int64_t row = (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l;
   if constexpr (MB > 0) {

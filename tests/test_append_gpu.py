@@ -107,6 +107,34 @@ def test_edge_vectors(device):
         assert np.array_equal(norms.cpu().numpy(), wn), bits
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_division_edge_vectors(device, dtype):
+    # u = x / max(n, 1e-6) is formed from the reciprocal with one fma
+    # refinement except where the quotient or its residual could leave the
+    # normal range; these rows take each side of that switch and must stay
+    # bit-exact with the IEEE division of the oracle.
+    D = 128
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((1, 1, 8, D)).astype(np.float32)
+    x[0, 0, 0, :4] = [1e-36, -3e-38, 5e-39, 0.0]   # tiny elements beside normal ones
+    x[0, 0, 1] *= 1e30                             # squares overflow: inf norm
+    x[0, 0, 2] = 1e-31                             # every element below 2^-100
+    x[0, 0, 3, ::3] = 0.0                          # zeros between normal values
+    x[0, 0, 4] *= 2.0 ** -90                       # small but on the fast side
+    x[0, 0, 5] = 1.0                               # all equal: |x| / n = 2^-3.5
+    x[0, 0, 6, 0] = 7.0                            # one-hot
+    xt = torch.from_numpy(x).to(dtype)
+    xin = xt.float().numpy()
+    for bits in (1, 3, 4):
+        codec = ops.Codec(D, bits, 2)
+        packed, norms = _buffers(1, 1, 8, codec, torch.float32, device)
+        ops.append_quantize(xt.to(device), codec, packed, norms, 0)
+        with np.errstate(over="ignore", invalid="ignore"):  # row 1's squares overflow to an inf norm
+            wp, wn = O.quantize_rht(xin, bits, O.rht_signs(D, 2), O.beta_codebook(D, bits))
+        assert np.array_equal(_np_u32(packed), wp), (dtype, bits)
+        assert np.array_equal(norms.cpu().numpy(), wn), (dtype, bits)
+
+
 def test_config0_full_layer_bit_exact(device):
     """K and V f16 [1, 8, 4096, 128], per-channel log-normal scales, 3-bit."""
     rs, rk, rv = (np.random.default_rng(s) for s in (1000, 1001, 1002))
