@@ -155,8 +155,8 @@ int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed, const void
                        const float* projection, float* out, void* stream);
 
 /*
- * Bytes of workspace tq_attention() needs for this problem (split-K partials,
- * rotated queries and merge counters).  max_tokens is the largest
+ * Bytes of workspace tq_attention() needs for this problem (split-K partials
+ * and rotated queries).  max_tokens is the largest
  * per-sequence cache length.
  */
 int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
@@ -184,10 +184,8 @@ int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
  *   array of B lengths, each <= max_tokens (ragged batches).
  * q: [B, Hq, L, dim] with element strides; out: contiguous [B, Hq, L, dim].
  * dim in {64, 128, 256}; L >= 1; Hq % Hkv == 0.
- * workspace: >= tq_attention_workspace_size() bytes, 256-byte aligned.  Its
- *   first 64 KiB hold merge counters that must be zero before the first call
- *   that uses this workspace (zero it once, e.g. with hipMemset); every call
- *   leaves them zero again, whatever the shapes of later calls.  Calls that
+ * workspace: >= tq_attention_workspace_size() bytes, 256-byte aligned, no
+ *   initial contents needed (a call overwrites what it reads).  Calls that
  *   may run concurrently (other streams) must use different workspaces.
  */
 int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,

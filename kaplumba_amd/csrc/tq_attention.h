@@ -23,10 +23,9 @@ namespace tq {
 // epilogue (wave combine, partial write) in series.
 constexpr int kMaxChunk = 1 << 20;
 constexpr int kMaxSplits = 1024;  // splits per sequence
-// The workspace starts with a fixed 64 KiB region the C ABI documents as
-// zero-initialised counters; the current kernels leave it untouched.
+// (sequence, kv head, row group) groups of one call: bounds the partial
+// buffers of the workspace
 constexpr int kMaxGroups = 16384;
-constexpr int64_t kCounterBytes = kMaxGroups * 4;
 
 struct AttnParams {
   // queries
@@ -55,7 +54,6 @@ struct AttnParams {
   // split-K
   int n_splits, chunk, n_rg, nq;  // nq: rows per row group
   // workspace
-  uint32_t* counters;  // reserved region at the workspace start
   float* qrot;         // [B, Hq, L, D] (dense rotation only)
   float* po;           // [B, Hq, L, n_splits, D]
   float* pml;          // [B, Hq, L, n_splits, 2]

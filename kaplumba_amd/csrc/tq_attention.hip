@@ -164,12 +164,12 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
 
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Layout: [counters kCounterBytes][q_rot B*Hq*L*D][partial o groups*splits*nq*D]
+// Layout: [q_rot B*Hq*L*D][partial o groups*splits*nq*D]
 // [partial (m, l) groups*splits*nq*2], groups = B * Hkv * n_rg.
 int64_t workspace_bytes(const SplitPlan& sp, int B, int Hq, int Hkv, int L, int D) {
   const int64_t rows = static_cast<int64_t>(B) * Hq * L;
   const int64_t grows = static_cast<int64_t>(B) * Hkv * sp.n_rg * sp.nq;  // padded rows
-  return kCounterBytes + align256(rows * D * 4) + align256(grows * sp.n_splits * D * 4) +
+  return align256(rows * D * 4) + align256(grows * sp.n_splits * D * 4) +
          align256(grows * sp.n_splits * 2 * 4);
 }
 
@@ -311,8 +311,6 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   p.nq = sp.nq;
   const int64_t rows = static_cast<int64_t>(B) * Hq * L;
   char* ws = static_cast<char*>(workspace);
-  p.counters = reinterpret_cast<uint32_t*>(ws);
-  ws += kCounterBytes;
   p.qrot = reinterpret_cast<float*>(ws);
   ws += (rows * dim * 4 + 255) / 256 * 256;
   p.po = reinterpret_cast<float*>(ws);

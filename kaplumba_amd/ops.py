@@ -219,9 +219,9 @@ _WORKSPACES: Dict[tuple, torch.Tensor] = {}
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Persistent attention workspace per (device, stream).
 
-    The kernel keeps merge counters at the head of the workspace and needs
-    them zero on entry; it resets them before returning, so a buffer zeroed
-    once at allocation stays valid for every later call on that stream.
+    The kernels write every workspace byte they read (rotated queries and
+    split partials), so one buffer serves every later call on that stream,
+    whatever the shapes; calls on other streams get their own.
     """
     key = (str(device), torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)

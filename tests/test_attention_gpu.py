@@ -252,8 +252,8 @@ def test_empty_cache_gives_zeros(device):
     assert out.shape == (1, 8, 1, 128) and not out.float().abs().sum().item()
 
 
-def test_repeated_calls_reuse_workspace_counters(device):
-    """The merge counters must come back to zero: run shapes of different group counts."""
+def test_repeated_calls_reuse_workspace(device):
+    """One cached workspace serves calls of different group and split counts in turn."""
     for B, Hkv, T in ((1, 2, 300), (3, 8, 5000), (1, 2, 300), (2, 4, 70)):
         run_case(device, B * 13 + T, B, Hkv * 4, Hkv, 1, T, 128, 3, 3)
 
