@@ -57,6 +57,25 @@ def test_prod_quantize_matches_oracle(device, d, bits):
     assert not st.qjl_signs.cpu().numpy()[:, :, 4 + L:].any()
 
 
+@pytest.mark.parametrize("bits", [3, 4])
+def test_prod_quantize_division_edge_rows(device, bits):
+    # f32 rows on both sides of the quotient method's switch (elements below
+    # 2^-100 take the IEEE division itself): norms and MSE indices bit-exact.
+    d = 128
+    rng = np.random.default_rng(90 + bits)
+    x = rng.standard_normal((1, 2, 6, d)).astype(np.float32)
+    x[0, 0, 0, :3] = [1e-36, -4e-39, 0.0]      # tiny elements beside normal ones
+    x[0, 0, 1] = 3e-32                         # every element below 2^-100
+    x[0, 0, 2, ::2] = 0.0                      # zeros between normal values
+    x[0, 1, 3] *= 2.0 ** -95                   # small, fast side of the switch
+    codec = ProdCodec(d, bits, 0)
+    st = codec.alloc(1, 2, 6, device, torch.float32)
+    codec.quantize_into(torch.from_numpy(x).to(device), st, 0)
+    n, mse, rn, sg, proj = _oracle(x, codec, "float32")
+    assert np.array_equal(st.norms.cpu().numpy(), n)
+    assert np.array_equal(st.mse_indices.cpu().numpy().astype(np.uint32), mse)
+
+
 def test_prod_quantize_f16_norms_bf16_input(device):
     rng = np.random.default_rng(3)
     x = torch.from_numpy(rng.standard_normal((1, 2, 33, 128)).astype(np.float32)).to(torch.bfloat16)
