@@ -31,8 +31,8 @@ import torch
 
 from . import ops
 from .cache import (KVCache, TurboQuantKVCache, TurboQuantMSEState, _BaseCache,
-                    _mask_is_causal, _QuantizedStateProxy, _unwrap, _validate_bits,
-                    create_causal_mask)
+                    _codec_meta_fields, _mask_is_causal, _parse_codec_meta_fields,
+                    _QuantizedStateProxy, _unwrap, _validate_bits, create_causal_mask)
 from .codebook import DEFAULT_TURBOQUANT_SEED
 
 __all__ = ["BatchTurboQuantKVCache", "BatchKVCache"]
@@ -96,6 +96,8 @@ class BatchTurboQuantKVCache(_LeftPadded, _BaseCache):
         self.bits = _validate_bits(bits)
         self.seed = seed
         TurboQuantKVCache(bits=self.bits, seed=seed, **turbo_kwargs)  # validates the options
+        if turbo_kwargs.get("key_quantizer", "mse") != "mse":
+            raise ValueError("BatchTurboQuantKVCache holds MSE-coded keys only")
         self._turbo_kwargs: Dict[str, Any] = dict(turbo_kwargs)
         self.keys: Optional[TurboQuantMSEState] = None
         self.values: Optional[TurboQuantMSEState] = None
@@ -229,6 +231,9 @@ class BatchTurboQuantKVCache(_LeftPadded, _BaseCache):
                     and self.value_codec.dim == other.value_codec.dim
                     and self.seed == other.seed
                     and self.key_codec.rotation == other.key_codec.rotation
+                    and self.value_codec.rotation == other.value_codec.rotation
+                    and self.key_codec.codebook_kind == other.key_codec.codebook_kind
+                    and self.value_codec.codebook_kind == other.value_codec.codebook_kind
                     and tuple(self.keys.norms.shape[1:2]) == tuple(other.keys.norms.shape[1:2])
                     and self.keys.norms.dtype == other.keys.norms.dtype)
             if not same:
@@ -316,11 +321,15 @@ class BatchTurboQuantKVCache(_LeftPadded, _BaseCache):
 
     @property
     def meta_state(self):
-        """(_idx, bits, seed, k_dim, v_dim) as strings; the reference stores the
-        first three (turboquant_cache.py:6282-6290) and a loader accepts both."""
+        """(_idx, bits, seed, k_dim, v_dim) as strings, then the codec options
+        (key_quantizer, key_bits, val_bits, rotation, codebook).  The reference
+        stores the first three (turboquant_cache.py:6282-6290) and reads only
+        those, so a loader accepts either form."""
         kd = self.key_codec.dim if self.key_codec else self._dims[0]
         vd = self.value_codec.dim if self.value_codec else self._dims[1]
-        return tuple(map(str, (self._idx, self.bits, self.seed, kd, vd)))
+        tmp = TurboQuantKVCache(bits=self.bits, seed=self.seed, **self._codec_kwargs())
+        return tuple(map(str, (self._idx, self.bits, self.seed, kd, vd) + _codec_meta_fields(
+            tmp.key_quantizer, *tmp._side_bits(), tmp.rotation, tmp.codebook_kind)))
 
     @meta_state.setter
     def meta_state(self, v):
@@ -329,6 +338,17 @@ class BatchTurboQuantKVCache(_LeftPadded, _BaseCache):
         self.seed = int(float(v[2]))
         if len(v) >= 5:
             self._dims = (int(float(v[3])), int(float(v[4])))
+        opts = _parse_codec_meta_fields(v[5:])
+        if opts.get("key_quantizer", "mse") != "mse":
+            raise ValueError("BatchTurboQuantKVCache holds MSE-coded keys only")
+        opts.pop("key_quantizer", None)
+        if opts:
+            self._turbo_kwargs.update(opts)
+            self.key_codec = self.value_codec = None  # rebuilt from the restored options
+
+    def _codec_kwargs(self) -> Dict[str, Any]:
+        """The codec options of _turbo_kwargs (norm_dtype lives in the state)."""
+        return {k: v for k, v in self._turbo_kwargs.items() if k != "norm_dtype"}
 
     @classmethod
     def from_state(cls, state, meta_state):

@@ -81,6 +81,40 @@ def _unwrap(state):
     return state._state if isinstance(state, _QuantizedStateProxy) else state
 
 
+def _codec_meta_fields(key_quantizer: str, key_bits: int, val_bits: int, rotation: str,
+                       codebook: str) -> tuple:
+    """The codec options a saved TurboQuant cache carries after the reference's
+    meta fields: (key_quantizer, key_bits, val_bits, rotation, codebook)."""
+    return (key_quantizer, int(key_bits), int(val_bits), rotation, codebook)
+
+
+def _parse_codec_meta_fields(extra) -> Dict[str, Any]:
+    """Options from the fields after (offset, bits, seed, k_dim, v_dim).
+
+    Accepts none (the reference's files), one (the key quantizer alone) or all
+    five; anything else is a malformed file.
+    """
+    extra = list(extra)
+    if not extra:
+        return {}
+    opts: Dict[str, Any] = {"key_quantizer": extra[0]}
+    if extra[0] not in ("mse", "prod"):
+        raise ValueError(f"unknown TurboQuant key quantizer {extra[0]!r} in meta_state")
+    if len(extra) == 1:
+        return opts
+    if len(extra) != 5:
+        raise ValueError(f"TurboQuant meta_state has {5 + len(extra)} fields; expected 5, 6 or 10")
+    kb, vb = int(float(extra[1])), int(float(extra[2]))
+    if not (1 <= kb <= 4 and 1 <= vb <= 4):
+        raise ValueError(f"TurboQuant meta_state bits {kb}/{vb} not in 1..4")
+    if extra[3] not in ("auto", "hadamard", "dense"):
+        raise ValueError(f"unknown rotation {extra[3]!r} in meta_state")
+    if extra[4] not in ("beta", "gaussian"):
+        raise ValueError(f"unknown codebook {extra[4]!r} in meta_state")
+    opts.update(key_bits=kb, val_bits=vb, rotation=extra[3], codebook=extra[4])
+    return opts
+
+
 def _mask_is_causal(mask, n_queries: int) -> bool:
     """None / "causal" masks; other masks are rejected (array masks are not built)."""
     if mask is None:
@@ -389,12 +423,17 @@ class TurboQuantKVCache(_BaseCache):
 
     @property
     def meta_state(self):
-        """(offset, bits, seed, k_dim, v_dim) as strings (turboquant_cache.py:6046-6050)."""
+        """(offset, bits, seed, k_dim, v_dim) as strings (turboquant_cache.py:6046-6050),
+        then the codec options: (key_quantizer, key_bits, val_bits, rotation, codebook).
+
+        The reference's five fields come first and its setter reads only the
+        first three, so files stay readable both ways; the trailing fields let
+        a cache built with non-default codecs reload with the same codecs.
+        """
         k_dim = self.key_codec.dim if self.key_codec else self._dims[0]
         v_dim = self.value_codec.dim if self.value_codec else self._dims[1]
-        fields = (self.offset, self.bits, self.seed, k_dim, v_dim)
-        if self.key_quantizer == "prod":  # an extra field only for Prod keys
-            fields += ("prod",)
+        fields = (self.offset, self.bits, self.seed, k_dim, v_dim) + _codec_meta_fields(
+            self.key_quantizer, *self._side_bits(), self.rotation, self.codebook_kind)
         return tuple(map(str, fields))
 
     @meta_state.setter
@@ -404,8 +443,14 @@ class TurboQuantKVCache(_BaseCache):
         self.seed = int(float(value[2]))
         if len(value) >= 5:
             self._dims = (int(float(value[3])), int(float(value[4])))
-        if len(value) >= 6:
-            self.key_quantizer = value[5]
+        opts = _parse_codec_meta_fields(value[5:])
+        if opts:
+            self.key_quantizer = opts.get("key_quantizer", self.key_quantizer)
+            self.key_bits_override = opts.get("key_bits", self.key_bits_override)
+            self.val_bits_override = opts.get("val_bits", self.val_bits_override)
+            self.rotation = opts.get("rotation", self.rotation)
+            self.codebook_kind = opts.get("codebook", self.codebook_kind)
+            self.key_codec = self.value_codec = None  # rebuilt from the restored options
 
     def is_trimmable(self):
         return True

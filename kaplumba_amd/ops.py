@@ -214,6 +214,10 @@ def dequantize(indices: torch.Tensor, norms: torch.Tensor, codec: Codec) -> torc
 
 
 _WORKSPACES: Dict[tuple, torch.Tensor] = {}
+# Workspaces replaced by a larger one.  They are never freed: a HIP graph
+# captured while one of them was current still holds its address, and a replay
+# must not write into memory the allocator has handed to another tensor.
+_RETIRED_WORKSPACES: list = []
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -221,14 +225,30 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
     The kernels write every workspace byte they read (rotated queries and
     split partials), so one buffer serves every later call on that stream,
-    whatever the shapes; calls on other streams get their own.
+    whatever the shapes, and needs no initial contents; calls on other
+    streams get their own.  A request beyond the current size allocates a
+    larger buffer and keeps the old one alive (see _RETIRED_WORKSPACES);
+    ``reserve_workspace`` sizes it once before graph capture.
     """
     key = (str(device), torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def reserve_workspace(device, B: int, Hq: int, Hkv: int, L: int, dim: int,
+                      max_tokens: int) -> int:
+    """Size the current stream's attention workspace for the largest problem a
+    caller will run (for example before capturing decode graphs for several
+    batch sizes), so no later call on that stream replaces it.  Returns bytes."""
+    device = torch.device(device)
+    nbytes = int(_lib.load().tq_attention_workspace_size(B, Hq, Hkv, L, dim, max_tokens))
+    _workspace(device, nbytes)
+    return nbytes
 
 
 def _seq_array(x, B: int, device) -> Optional[torch.Tensor]:

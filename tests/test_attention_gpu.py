@@ -258,6 +258,39 @@ def test_repeated_calls_reuse_workspace(device):
         run_case(device, B * 13 + T, B, Hkv * 4, Hkv, 1, T, 128, 3, 3)
 
 
+def test_graph_survives_a_larger_workspace(device):
+    """A graph captured on a stream keeps its workspace address.  A later,
+    larger call on that stream moves the stream to a new workspace; the old
+    one must stay allocated, so replaying the graph still gives its eager
+    output (and a tensor allocated meanwhile is not overwritten)."""
+    kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)
+
+    def problem(seed, B, Hkv, T):
+        q, kp, kn, vp, vn, _, _ = build_case(seed, B, 4 * Hkv, Hkv, 1, T, 128, 3, 3)
+        return q_tensor(q, "bf16", device), to_buffers(kp, kn, vp, vn, device)
+
+    s = torch.cuda.Stream(device=device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    small_q, small_kv = problem(1, 1, 2, 700)
+    big_q, big_kv = problem(2, 4, 8, 20000)
+    with torch.cuda.stream(s):
+        call = lambda q, kv: ops.attention_packed(q, kv[0], kv[1], kv[2], kv[3], kc, vc, 0.088, False)
+        eager = call(small_q, small_kv)  # workspace sized for the small problem
+        torch.cuda.synchronize(device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            captured = call(small_q, small_kv)
+        big = call(big_q, big_kv)        # needs a larger workspace on this stream
+        guard = torch.full((1 << 22,), 3.0, device=device)
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize(device)
+            assert torch.equal(captured, eager)
+            assert bool((guard == 3.0).all())
+    torch.cuda.synchronize(device)
+    assert torch.equal(call(big_q, big_kv), big)
+
+
 def test_config1_full_size(device):
     """Config 1: 32 q heads / 8 kv heads, d=128, 32768 tokens, 3-bit, bf16 query.
 

@@ -137,6 +137,37 @@ def test_extend_rejects_mismatched_codecs():
         ca.extend(cb)
 
 
+def test_extend_rejects_mismatched_codebooks():
+    """Rows coded with another codebook would decode wrongly after a merge."""
+    ca = synth_tq([0], 4)
+    cb = synth_tq([0], 4)
+    cb._turbo_kwargs["codebook"] = "gaussian"
+    cb.key_codec = cb.value_codec = None
+    with pytest.raises(ValueError):
+        ca.extend(cb)
+    with pytest.raises(ValueError):
+        BatchTurboQuantKVCache([0], bits=3, key_quantizer="prod")
+
+
+def test_save_load_keeps_codec_options_batch():
+    c = BatchTurboQuantKVCache([1, 0], bits=3, rotation="dense", codebook="gaussian",
+                               key_bits=4, val_bits=2)
+    g = torch.Generator().manual_seed(3)
+    mk = lambda pw: TurboQuantMSEState(torch.rand(2, H, 5, generator=g),
+                                       torch.randint(0, 1 << 30, (2, H, 5, pw), generator=g).to(torch.uint32))
+    c.state = (mk(32), mk(16), torch.tensor([4, 5]), torch.tensor([1, 0]))
+    c.meta_state = ("5", "3.0", "0", "256", "256")  # dims only: the options stay
+    with tempfile.TemporaryDirectory() as td:
+        f = os.path.join(td, "c.safetensors")
+        save_prompt_cache(f, [c])
+        (r,) = load_prompt_cache(f, device="cpu")
+    assert r.meta_state == c.meta_state
+    r._codecs_ready()
+    assert (r.key_codec.bits, r.value_codec.bits) == (4, 2)
+    assert r.key_codec.rotation == "dense" and r.value_codec.codebook_kind == "gaussian"
+    assert r.key_codec.packed_width == r.state[0].indices.shape[-1]
+
+
 def test_save_load_round_trip_cpu():
     c = synth_tq([1, 0], 5)
     e = BatchTurboQuantKVCache([3], bits=3)

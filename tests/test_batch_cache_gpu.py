@@ -28,13 +28,16 @@ pytestmark = pytest.mark.gpu
     (32, 8, 4, 128, 2, 1, "hadamard"),   # 16-row groups
     (16, 8, 1, 256, 4, 2, "dense"),      # d = 256, dense rotation (query prep + dense merge)
 ])
-def test_ranged_packed_attention(device, Hq, Hkv, L, d, kb, vb, rot):
+@pytest.mark.parametrize("norm", ["float32", "float16"])
+def test_ranged_packed_attention(device, Hq, Hkv, L, d, kb, vb, rot, norm):
     # rows: no padding; padding inside the first split; one token left;
-    # nothing left (zero output); padding and a shorter end together
-    starts = [0, 700, 2599, 1000, 300]
-    lens = [2600, 2600, 2600, 1000, 2000]
+    # nothing left (zero output); padding and a shorter end together.  With
+    # f16 norms an odd start puts the row's norms at an address 2 mod 4, and
+    # odd ends exercise the last-token norm patch.
+    starts = [0, 700, 2599, 1000, 301]
+    lens = [2600, 2600, 2600, 1000, 2001]
     run_case(device, 7 + d + L, 5, Hq, Hkv, L, 2600, d, kb, vb, rot=rot, lengths=lens,
-             starts=starts)
+             starts=starts, norm=norm)
 
 
 @pytest.mark.parametrize("L", [1, 3])

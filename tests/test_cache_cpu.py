@@ -51,7 +51,8 @@ def test_state_setter_trim_meta_from_state():
     c.state = st
     c.meta_state = ("10", "3.0", "7", "64", "64")
     assert c.offset == 10 and not c.empty() and c.size() == 10
-    assert c.meta_state == ("10", "3.0", "7", "64", "64")
+    # the reference's five fields, then (key_quantizer, key_bits, val_bits, rotation, codebook)
+    assert c.meta_state == ("10", "3.0", "7", "64", "64", "mse", "3", "3", "auto", "beta")
     assert c.trim(3) == 3 and c.offset == 7 and c.state[0].norms.shape[2] == 7
     assert c.trim(100) == 7 and c.offset == 0
     r = TurboQuantKVCache.from_state(st, ("10", "3.0", "7", "64", "64"))
@@ -154,8 +155,8 @@ def test_prod_key_quantizer_options_and_meta_state():
         TurboQuantKVCache(bits=3, key_quantizer="qjl")
     with pytest.raises(ValueError):
         TurboQuantKVCache(bits=3, key_quantizer="prod", rotation="dense")
-    # meta_state gains a sixth field only for Prod keys, and a CPU state round trip keeps it
-    assert len(TurboQuantKVCache(bits=3).meta_state) == 5
+    # the key quantizer is the sixth field, and a CPU state round trip keeps it
+    assert TurboQuantKVCache(bits=3).meta_state[5] == "mse"
     from kaplumba_amd.prod import TurboQuantProdState
     st = (TurboQuantProdState(torch.ones(1, 2, 7), torch.zeros(1, 2, 7, 8, dtype=torch.uint32),
                               torch.ones(1, 2, 7), torch.zeros(1, 2, 7, 4, dtype=torch.uint32)),
@@ -163,3 +164,66 @@ def test_prod_key_quantizer_options_and_meta_state():
     c2 = TurboQuantKVCache.from_state(st, ("7", "3.0", "0", "128", "128", "prod"))
     assert c2.key_quantizer == "prod" and c2.offset == 7 and c2.meta_state[5] == "prod"
     assert isinstance(c2.state[0], TurboQuantProdState) and c2.nbytes > 0
+
+
+@pytest.mark.parametrize("opts", [
+    dict(bits=3, rotation="dense", codebook="gaussian", key_bits=4, val_bits=2),
+    dict(bits=3.5, codebook="gaussian"),
+    dict(bits=2, rotation="hadamard", key_bits=1),
+    dict(bits=3, key_quantizer="prod"),
+])
+def test_meta_state_restores_codec_options(opts):
+    """A cache rebuilt from (state, meta_state) builds the codecs the saved one
+    used: rotation, codebook and per-side widths (the reference keeps only
+    offset, bits and seed, turboquant_cache.py:6046-6056)."""
+    c = TurboQuantKVCache(seed=5, **opts)
+    c._build_codecs(256, 256)
+    r = TurboQuantKVCache.from_state([], c.meta_state)
+    r._dims = (256, 256)
+    r._ensure_codecs_from_meta()
+    assert r.meta_state == c.meta_state
+    assert type(r.key_codec) is type(c.key_codec)
+    for a, b in ((r.key_codec, c.key_codec), (r.value_codec, c.value_codec)):
+        assert (a.dim, a.bits, a.seed) == (b.dim, b.bits, b.seed)
+        if isinstance(a, ops.Codec):
+            assert (a.rotation, a.codebook_kind) == (b.rotation, b.codebook_kind)
+            assert np.array_equal(a.codebook, b.codebook)
+
+
+def test_meta_state_reference_and_round1_forms():
+    """Five fields (the reference's files) give the default codecs; six carry
+    the key quantizer alone; other lengths and unknown values are refused."""
+    r = TurboQuantKVCache.from_state([], ("0", "3.0", "0", "128", "128"))
+    r._ensure_codecs_from_meta()
+    assert (r.key_codec.rotation, r.key_codec.codebook_kind, r.key_codec.bits) == ("hadamard", "beta", 3)
+    r = TurboQuantKVCache.from_state([], ("0", "3.0", "0", "128", "128", "prod"))
+    assert r.key_quantizer == "prod"
+    for bad in [("0", "3", "0", "128", "128", "mse", "3"),
+                ("0", "3", "0", "128", "128", "qjl"),
+                ("0", "3", "0", "128", "128", "mse", "3", "3", "givens", "beta"),
+                ("0", "3", "0", "128", "128", "mse", "3", "3", "dense", "uniform"),
+                ("0", "3", "0", "128", "128", "mse", "5", "3", "dense", "beta")]:
+        with pytest.raises(ValueError):
+            TurboQuantKVCache.from_state([], bad)
+
+
+def test_save_load_keeps_codec_options():
+    """Through a prompt-cache file: a dense / Gaussian K4-V2 cache comes back
+    with the same codecs (its packed widths match the saved rows)."""
+    c = TurboQuantKVCache(bits=3, seed=2, rotation="dense", codebook="gaussian", key_bits=4, val_bits=2)
+    c._build_codecs(256, 256)
+    g = torch.Generator().manual_seed(1)
+    mk = lambda pw: TurboQuantMSEState(torch.rand(1, 2, 9, generator=g),
+                                       torch.randint(0, 1 << 30, (1, 2, 9, pw), generator=g).to(torch.uint32))
+    c.state = (mk(32), mk(16))
+    with tempfile.TemporaryDirectory() as d:
+        f = os.path.join(d, "c.safetensors")
+        save_prompt_cache(f, [c])
+        (r,) = load_prompt_cache(f, device="cpu")
+    r._ensure_codecs_from_meta()
+    assert (r.key_codec.bits, r.value_codec.bits) == (4, 2)
+    assert r.key_codec.rotation == r.value_codec.rotation == "dense"
+    assert r.key_codec.codebook_kind == "gaussian" and r.seed == 2
+    assert r.key_codec.packed_width == r.state[0].indices.shape[-1]
+    assert r.value_codec.packed_width == r.state[1].indices.shape[-1]
+    assert torch.equal(r.state[0].indices, c.state[0].indices)
