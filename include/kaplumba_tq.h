@@ -247,6 +247,31 @@ int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
                       int causal, void* out, void* workspace, int64_t workspace_bytes,
                       void* stream);
 
+/*
+ * tq_attention_ranged without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, which
+ * never exposes a workspace.  The split partials and rotated queries live in
+ * a static device array of TQ_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends; the entry point calls no hipMalloc / hipFree.  Problems whose
+ * tq_attention_workspace_size() exceeds that size return TQ_ERR_WORKSPACE
+ * (use tq_attention with a caller workspace).  Every call on one GPU shares
+ * the array: calls that overlap on that GPU (other streams, other host
+ * threads) race.  No initial contents are needed: a call writes every
+ * scratch byte it reads.  Every other argument and the results are those of
+ * tq_attention_ranged.
+ */
+#define TQ_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int tq_attention_noalloc(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
+                         int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
+                         int kv_kind, int kv_dtype,
+                         const void* k, const void* k_norms, const void* v, const void* v_norms,
+                         int norm_dtype, int k_bits, int v_bits,
+                         const float* k_codebook, const float* v_codebook,
+                         int rot_kind, const float* k_rot, const float* v_rot,
+                         int64_t capacity, int64_t max_tokens, const int32_t* seq_starts,
+                         const int32_t* seq_lens, int causal, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -90,7 +90,20 @@ SIGNATURES = {
         c_int, c_void_p, c_void_p,
         c_int64, c_int64, c_void_p, c_void_p, c_int,           # ..., seq_starts, seq_lens, causal
         c_void_p, c_void_p, c_int64, c_void_p]),
+    "tq_attention_noalloc": (c_int, [
+        c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+        c_int64, c_int64, c_int64, c_float,
+        c_int, c_int,
+        c_void_p, c_void_p, c_void_p, c_void_p,
+        c_int, c_int, c_int,
+        c_void_p, c_void_p,
+        c_int, c_void_p, c_void_p,
+        c_int64, c_int64, c_void_p, c_void_p, c_int,           # ..., seq_starts, seq_lens, causal
+        c_void_p, c_void_p]),                                  # out, stream (static scratch)
 }
+
+# Scratch bytes of tq_attention_noalloc (TQ_NOALLOC_SCRATCH_BYTES in the header).
+TQ_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 
 class TurboQuantLibraryError(RuntimeError):

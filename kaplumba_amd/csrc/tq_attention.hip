@@ -2,6 +2,7 @@
 // attention.  The attention work itself is the fused kernel of tq_attn_impl.h.
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 #include "tq_attn_splitmerge.h"
 
@@ -400,6 +401,70 @@ extern "C" int tq_attention(const void* q, int q_dtype, int B, int Hq, int Hkv, 
                              v_bits, k_codebook, v_codebook, rot_kind, k_rot, v_rot, capacity,
                              max_tokens, nullptr, seq_lens, causal, out, workspace,
                              workspace_bytes_given, stream);
+}
+
+// ------------------------------------------------------------ no-alloc ----
+// Attention scratch for callers that cannot allocate (graph capture, serving
+// loops).  Each device holds its own copy of this array for the life of the
+// process.  In host code `scratch` names a host-side stand-in, not device
+// memory: kernels and copies take the per-device address from
+// hipGetSymbolAddress instead.
+namespace {
+
+constexpr int64_t kScratchBytes = TQ_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's scratch address, looked up once per device (with that
+// device current) and kept.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TQ_ERR_HIP, "attention (no-alloc): hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(TQ_ERR_UNSUPPORTED, "attention (no-alloc): device %d beyond %d", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(TQ_ERR_HIP, "attention (no-alloc): hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" int tq_attention_noalloc(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
+                                    int dim, int64_t q_stride_b, int64_t q_stride_h,
+                                    int64_t q_stride_l, float scale, int kv_kind, int kv_dtype,
+                                    const void* k, const void* k_norms, const void* v,
+                                    const void* v_norms, int norm_dtype, int k_bits, int v_bits,
+                                    const float* k_codebook, const float* v_codebook, int rot_kind,
+                                    const float* k_rot, const float* v_rot, int64_t capacity,
+                                    int64_t max_tokens, const int32_t* seq_starts,
+                                    const int32_t* seq_lens, int causal, void* out, void* stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || L < 1 || dim <= 0 || max_tokens < 0 || Hq % Hkv)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "attention (no-alloc): bad shape (B %d, Hq %d, Hkv %d, L %d, dim %d)",
+                B, Hq, Hkv, L, dim);
+  if (B == 0) return TQ_OK;
+  const int64_t need = tq_attention_workspace_size(B, Hq, Hkv, L, dim, max_tokens);
+  if (need > kScratchBytes)
+    return fail(TQ_ERR_WORKSPACE, "attention (no-alloc): the problem needs %lld bytes of scratch, "
+                "above the static %lld; use tq_attention with a caller workspace",
+                (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return tq_attention_ranged(q, q_dtype, B, Hq, Hkv, L, dim, q_stride_b, q_stride_h, q_stride_l,
+                             scale, kv_kind, kv_dtype, k, k_norms, v, v_norms, norm_dtype, k_bits,
+                             v_bits, k_codebook, v_codebook, rot_kind, k_rot, v_rot, capacity,
+                             max_tokens, seq_starts, seq_lens, causal, out, ws, kScratchBytes, stream);
 }
 
 extern "C" int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
