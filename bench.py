@@ -134,8 +134,11 @@ def bench_decode(torch, args, dev):
     for i in (0, args.steps - 1):
         if not torch.equal(outs[i], step(i)):
             raise RuntimeError(f"graph replay of step {i} differs from the eager call")
+    (kn, kp), (vn, vp) = layers[0]
+    host = lambda t: t.cpu().numpy()
+    sample = (qs[0].float().cpu().numpy(), host(kp), host(kn), host(vp), host(vn))
     return dict(bytes=per_layer, ms_per_step=ms, n_layers=n_layers,
-                rotate_mb=n_layers * per_layer / 1e6)
+                rotate_mb=n_layers * per_layer / 1e6, cpu_sample=sample)
 
 
 def bench_quantize(torch, args, dev):
@@ -443,37 +446,60 @@ def bench_prod_decode(torch, args, dev):
             "steps": steps}
 
 
-def cpu_baseline(seconds_budget=12.0):
-    """Numpy restatement of the reference's array-path attention (oracle), cfg1 shape."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(sample, seconds_budget=12.0):
+    """The reference's array-path attention (oracle restatements) on the host.
+
+    ``sample`` is the first layer cache of the headline leg copied to host
+    memory (the append kernel's bytes, which equal the oracle quantizer's), so
+    the CPU works on exactly the cfg1 workload: 8 kv heads x 32768 tokens.
+    The torch-CPU restatement runs on all the threads torch is given (the
+    figure reported); the numpy restatement runs once, single-threaded, beside it.
+    """
     import numpy as np
+    import torch
 
     from oracle import tq_oracle as O
+    from oracle import tq_oracle_torch as OT
 
     c = CFG1
-    T = 8192  # bounded sample: a quarter of the context, same heads and widths
-    rng = np.random.default_rng(1001)
-    pw = (c["D"] * c["bits"] + 31) // 32
-    kp = rng.integers(0, 2 ** 32, size=(1, c["Hkv"], T, pw), dtype=np.uint64).astype(np.uint32)
-    vp = rng.integers(0, 2 ** 32, size=(1, c["Hkv"], T, pw), dtype=np.uint64).astype(np.uint32)
-    kn = rng.uniform(10, 20, size=(1, c["Hkv"], T)).astype(np.float32)
-    vn = rng.uniform(10, 20, size=(1, c["Hkv"], T)).astype(np.float32)
-    q = O.round_to_dtype(rng.standard_normal((1, c["Hq"], 1, c["D"])).astype(np.float32), "bf16")
+    q, kp, kn, vp, vn = sample
+    T = kp.shape[2]
     cb = O.beta_codebook(c["D"], c["bits"])
+    kw = dict(k_bits=c["bits"], v_bits=c["bits"], k_codebook=cb, v_codebook=cb,
+              signs_k=O.rht_signs(c["D"], 0), signs_v=O.rht_signs(c["D"], 1),
+              scale=1 / math.sqrt(c["D"]), q_dtype="bf16")
+    threads = torch.get_num_threads()
     runs = []
     t_start = time.perf_counter()
-    while len(runs) < 3 or (time.perf_counter() - t_start < seconds_budget and len(runs) < 20):
+    while len(runs) < 3 or (time.perf_counter() - t_start < seconds_budget and len(runs) < 30):
         t0 = time.perf_counter()
-        O.attention_chunked_f32(q, kp, kn, vp, vn, k_bits=3, v_bits=3, k_codebook=cb, v_codebook=cb,
-                                signs_k=O.rht_signs(c["D"], 0), signs_v=O.rht_signs(c["D"], 1),
-                                scale=1 / math.sqrt(c["D"]), q_dtype="bf16",
-                                key_chunk=1 << 30)
+        OT.attention_chunked(q, kp, kn, vp, vn, key_chunk=1 << 30, **kw)
         runs.append(time.perf_counter() - t0)
     med = sorted(runs)[len(runs) // 2]
-    gbs = algorithmic_decode_bytes(c["Hkv"], T, c["D"], 3, 3, 4) / med / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle (reference array-path attention, f32) at cfg1 heads/dims with "
-                      f"T={T} tokens, median of {len(runs)} runs ({med * 1e3:.0f} ms each); "
-                      "reference algorithm, numpy restatement -- not MLX"}
+    t0 = time.perf_counter()
+    O.attention_chunked_f32(q, kp, kn, vp, vn, key_chunk=1 << 30, **kw)
+    t_np = time.perf_counter() - t0
+    nbytes = algorithmic_decode_bytes(c["Hkv"], T, c["D"], c["bits"], c["bits"], 4)
+    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu": _cpu_model(), "host_cores_visible": len(os.sched_getaffinity(0)),
+            "torch_threads": threads, "ms_per_step": round(med * 1e3, 2),
+            "numpy_single_thread": {"value": round(nbytes / t_np / 1e9, 4), "unit": "GB/s",
+                                    "ms_per_step": round(t_np * 1e3, 1)},
+            "sample": f"the cfg1 workload itself: one layer cache (8 kv heads x {T} tokens, 3-bit, "
+                      f"f32 norms) and its bf16 query, attention by the torch-CPU restatement of the "
+                      f"reference array path (oracle/tq_oracle_torch.py) on {threads} threads, median "
+                      f"of {len(runs)} runs; reference algorithm, torch/numpy restatement -- not MLX"}
 
 
 def main():
@@ -532,7 +558,10 @@ def main():
                      "traffic_note": "HBM bytes per call from rocprofv3 FETCH_SIZE/WRITE_SIZE, "
                                      "copy-calibrated; algorithmic bytes are 27,262,976",
                      "kernel": "attention call: attn_small_kernel<128,3,3> + attn_merge_kernel<128>",
-                     "kernel_us": round(dec["ms_per_step"] * 1e3, 3)},
+                     "call_us": round(dec["ms_per_step"] * 1e3, 3),
+                     "achieved_note": "algorithmic bytes / time of one whole attention call (both "
+                                      "kernels, HIP events around a graph replay); the per-kernel "
+                                      "durations are in the committed rocprofv3 summaries"},
     }
     if "cfg0" in legs:
         qnt = bench_quantize(torch, args, dev)
@@ -553,7 +582,7 @@ def main():
     if "prod" in legs:
         line["prod_decode"] = bench_prod_decode(torch, args, dev)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"] = cpu_baseline(dec["cpu_sample"])
     print(json.dumps(line))
 
 

@@ -58,6 +58,7 @@ struct AttnParams {
   float* po;           // [B, Hq, L, n_splits, D]
   float* pml;          // [B, Hq, L, n_splits, 2]
   float rscale;        // f32(1/sqrt(D))
+  int merge_rot;       // Hadamard partials left in the rotated basis: the merge applies R_V^-1
   // Prod-coded keys (kv kind TQ_KV_PROD): k / kn are the MSE part at bits - 1
   const void* ksg;     // QJL sign rows [B, Hkv, cap, D / 32] u32
   const void* krn;     // residual norms [B, Hkv, cap] (norm_dtype)
@@ -94,6 +95,9 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
 // R <= 4, or verify with R * L <= 4) at head dim 64 / 128 run the small
 // row-group kernel (tq_attn_small.h).
 bool small_rows_path(int kv_kind, int D, int rows);
+// Of those, MSE-coded keys run the LDS-staged kernel of tq_attn_stage.h
+// (KAPLUMBA_TQ_STAGE=0 selects attn_small_kernel instead, for comparisons).
+bool stage_path();
 // Packed caches at head dim 128 with more rows run 16-row groups on the
 // register-softmax kernel of tq_attn_rows16.h.
 bool rows16_path(int kv_kind, int D, int rows);

@@ -119,6 +119,14 @@ bool small_rows_path(int kv_kind, int D, int rows) {
   return enabled && kv_kind == TQ_KV_PACKED && D <= 128 && rows <= 4;
 }
 
+bool stage_path() {
+  static const bool enabled = [] {
+    const char* e = getenv("KAPLUMBA_TQ_STAGE");
+    return !(e && e[0] == '0');
+  }();
+  return enabled;
+}
+
 bool rows16_path(int kv_kind, int D, int rows) {
   // KAPLUMBA_TQ_ROWS16=0 selects the general kernel instead
   static const bool enabled = [] {
@@ -321,6 +329,11 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   p.rscale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
+  // the staged row-group kernel leaves Hadamard partials in the rotated basis
+  p.merge_rot = (kv_kind == TQ_KV_PACKED && !prod && rot_kind == TQ_ROT_HADAMARD && stage_path() &&
+                 small_rows_path(kv_kind, dim, (Hq / Hkv) * L))
+                    ? 1
+                    : 0;
   int rc = TQ_OK;
   if (prod) {
     // q_proj = q_s @ P^T into the rotated-query region (unused by the Hadamard rotation)
@@ -356,6 +369,16 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   // the splits' partials are merged by a second kernel
   // one workgroup per query row; for the dense rotation one per 64 output
   // columns of a row group (R_V^-1 is read once per row group)
+  if (p.merge_rot) {
+    // the staged row-group kernel: 4-row groups, partials in the rotated basis
+    const dim3 rgrid(4, static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+    const int valid = (seq_starts || seq_lens) ? -1 : static_cast<int>((T + sp.chunk - 1) / sp.chunk);
+    switch (dim) {
+      case 64: hipLaunchKernelGGL(attn_merge_rot_kernel<64>, rgrid, dim3(kMergeThreads), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, p); break;
+      default: hipLaunchKernelGGL(attn_merge_rot_kernel<128>, rgrid, dim3(kMergeThreads), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, p); break;
+    }
+    return check_launch("attn_merge_rot_kernel");
+  }
   const unsigned mx = rot_kind == TQ_ROT_DENSE ? static_cast<unsigned>(dim / 64) : static_cast<unsigned>(sp.nq);
   const dim3 mgrid(mx, static_cast<unsigned>(Hkv * sp.n_rg), static_cast<unsigned>(B));
   switch (dim) {

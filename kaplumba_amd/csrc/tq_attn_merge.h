@@ -29,6 +29,52 @@ __device__ __forceinline__ void store_out(void* o, int dt, int64_t i, float v) {
 }
 
 
+// The two wave halves exchanged (v_permlane32_swap): .x = x of lane l for
+// l < 32 and of lane l - 32 otherwise, .y = x of lane l + 32 for l < 32 and
+// of lane l otherwise; so op(.x, .y) is the pairwise op of lanes l, l ^ 32.
+__device__ __forceinline__ float2 halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, xor_lane<1>(x));
+  x = fmaxf(x, xor_lane<2>(x));
+  x = fmaxf(x, xor_lane<4>(x));
+  x = fmaxf(x, xor_lane<8>(x));
+  x = fmaxf(x, xor_lane<16>(x));
+  const float2 h = halves(x);
+  return fmaxf(h.x, h.y);
+}
+
+// Unnormalised Walsh-Hadamard transform of a D-vector held by one wave as
+// y[e] = x[lane + 64 e]: butterflies across e in-lane, across lanes by DPP,
+// swizzles and the half swap.  sgn[k] = -1 where lane bit k is set, else 1.
+template <int D>
+__device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], const float (&sgn)[6]) {
+  constexpr int E = D / kWave;
+#pragma unroll
+  for (int s = E / 2; s >= 1; s >>= 1)
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if ((e & s) == 0) {
+        const float a = y[e], b = y[e + s];
+        y[e] = a + b;
+        y[e + s] = a - b;
+      }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    float v = y[e];
+    v = fmaf(sgn[0], v, xor_lane<1>(v));
+    v = fmaf(sgn[1], v, xor_lane<2>(v));
+    v = fmaf(sgn[2], v, xor_lane<4>(v));
+    v = fmaf(sgn[3], v, xor_lane<8>(v));
+    v = fmaf(sgn[4], v, xor_lane<16>(v));
+    const float2 h = halves(v);  // lanes < 32: v + v[l + 32]; others: v[l - 32] - v
+    y[e] = fmaf(sgn[5], h.y, h.x);
+  }
+}
+
 // In-place unnormalised Walsh-Hadamard transform of NQ rows of length D in
 // LDS (stride D), all NT threads of the block participating.
 template <int D, int NQ, int NT>

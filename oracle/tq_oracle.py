@@ -437,7 +437,8 @@ def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: n
                    v_norms: np.ndarray, *, k_bits: int, v_bits: int, k_signs_rot: np.ndarray,
                    k_mse_codebook: Optional[np.ndarray], proj: np.ndarray,
                    v_codebook: np.ndarray, v_rot: np.ndarray, scale: float, q_dtype: str,
-                   causal: bool = False, lengths: Optional[Sequence[int]] = None) -> np.ndarray:
+                   causal: bool = False, lengths: Optional[Sequence[int]] = None,
+                   starts: Optional[Sequence[int]] = None) -> np.ndarray:
     """Attention with Prod-coded keys and MSE-coded values, float64.
 
     Scores follow ``score_prepared`` (:4700-4766) -- ``n * q_rot . c[idx] +
@@ -458,13 +459,15 @@ def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: n
     fmin = float(np.finfo(np.float32).min)
     cap = kd_all.shape[2]
     for b in range(B):
-        T = cap if lengths is None else int(lengths[b])
+        end = cap if lengths is None else int(lengths[b])
+        t0 = 0 if starts is None else min(int(starts[b]), end)
+        T = end - t0
         if T == 0:
             continue
         for g in range(Hkv):
-            kd = kd_all[b, g, :T]
-            vidx = unpack_lowbit(v_packed[b, g, :T], v_bits, D)
-            vd = vc[vidx] * np.asarray(v_norms[b, g, :T], np.float64)[:, None]
+            kd = kd_all[b, g, t0:end]
+            vidx = unpack_lowbit(v_packed[b, g, t0:end], v_bits, D)
+            vd = vc[vidx] * np.asarray(v_norms[b, g, t0:end], np.float64)[:, None]
             for r in range(R):
                 h = g * R + r
                 s = qs[b, h] @ kd.T

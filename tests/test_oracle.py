@@ -293,6 +293,26 @@ def test_decode_is_last_causal_row_and_f32_chunked_agrees():
     np.testing.assert_allclose(f32, full, atol=2e-5)
 
 
+@pytest.mark.parametrize("kb,vb", [(3, 3), (2, 1), (4, 2), (1, 4)])
+def test_torch_cpu_baseline_equals_float64_oracle(kb, vb):
+    """The multi-threaded CPU baseline computes the oracle's attention."""
+    from oracle import tq_oracle_torch as OT
+
+    rng = np.random.default_rng(20 + kb)
+    B, Hq, Hkv, L, T, d = 1, 8, 2, 1, 3000, 128
+    q, kp, kn, vp, vn, kr, vr = _attn_case(rng, B, Hq, Hkv, L, T, d, kb, vb, "hadamard")
+    kw = dict(k_bits=kb, v_bits=vb, k_codebook=O.beta_codebook(d, kb),
+              v_codebook=O.beta_codebook(d, vb), scale=1 / math.sqrt(d), q_dtype="bf16")
+    want = O.attention(q, kp, kn, vp, vn, rot_kind="hadamard", k_rot=kr, v_rot=vr, **kw)
+    got = OT.attention_chunked(q, kp, kn, vp, vn, signs_k=kr, signs_v=vr, key_chunk=1024, **kw)
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    # the unpack agrees with the big-integer restatement's inverse on random words
+    words = rng.integers(0, 2 ** 32, size=(4, O.packed_width(d, kb)), dtype=np.uint64).astype(np.uint32)
+    np.testing.assert_array_equal(
+        OT.unpack_lowbit(torch.from_numpy(words.astype(np.int64)), kb, d).numpy(),
+        O.unpack_lowbit(words, kb, d))
+
+
 def test_ragged_lengths_equal_truncated_cache():
     rng = np.random.default_rng(13)
     B, Hq, Hkv, L, T, d = 2, 4, 2, 1, 50, 64
@@ -379,3 +399,64 @@ def test_prod_dequantize_is_an_unbiased_inner_product():
     est = kh @ q
     slope = float(est @ exact / (exact @ exact))
     assert abs(slope - 1.0) < 0.04, slope
+
+
+@pytest.mark.parametrize("bits", [2, 3, 1])
+def test_prod_attention_against_sdpa_and_score_prepared(bits):
+    """attention_prod equals (1) torch SDPA over the dequantized Prod keys
+    under an explicit causal + left-padding + length mask, and (2) a softmax
+    over scores formed the way score_prepared and the fused Prod decode kernel
+    form them (:4700-4766, :2000-2206): n * (R q_s) . c[idx] plus
+    n * rn * sqrt(pi/2)/d * (P q_s) . s, never building a key vector."""
+    rng = np.random.default_rng(30 + bits)
+    B, Hq, Hkv, L, T, d = 3, 4, 2, 3, 70, 64
+    sg, P = O.rht_signs(d, 0), O.projection_matrix(d, 1)
+    mcb = O.beta_codebook(d, bits - 1) if bits > 1 else None
+    k = rng.standard_normal((B, Hkv, T, d)).astype(np.float32)
+    n, mse, rn, sbits, _ = O.quantize_prod(k, bits, sg, mcb, P)
+    vp, vn = O.quantize_rht(rng.standard_normal((B, Hkv, T, d)).astype(np.float32), 2,
+                            O.rht_signs(d, 1), O.beta_codebook(d, 2))
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, d)).astype(np.float32), "bf16")
+    lengths, starts = [70, 41, 9], [0, 13, 9]
+    scale = 1 / math.sqrt(d)
+    got = O.attention_prod(q, n, mse, rn, sbits, vp, vn, k_bits=bits, v_bits=2, k_signs_rot=sg,
+                           k_mse_codebook=mcb, proj=P, v_codebook=O.beta_codebook(d, 2),
+                           v_rot=O.rht_signs(d, 1), scale=scale, q_dtype="bf16", causal=True,
+                           lengths=lengths, starts=starts)
+    # (1) SDPA with the boolean mask of create_causal_mask(left_padding=...) plus the lengths
+    K = O.prod_key_vectors(n, mse, rn, sbits, bits=bits, dim=d, signs=sg, mse_codebook=mcb, proj=P)
+    V = O.dequantize(vp, vn, 2, d, O.beta_codebook(d, 2), "hadamard", O.rht_signs(d, 1))
+    qs = torch.from_numpy(O.scale_queries(q, scale, "bf16").astype(np.float64))
+    R = Hq // Hkv
+    for b in range(B):
+        s0, e = starts[b], lengths[b]
+        if e == s0:
+            assert not got[b].any()
+            continue
+        kpos = torch.arange(T)
+        qpos = e - L + torch.arange(L)
+        mask = (kpos[None, :] <= qpos[:, None]) & (kpos[None, :] >= s0) & (kpos[None, :] < e)
+        Kt = torch.from_numpy(K[b]).repeat_interleave(R, dim=0)
+        Vt = torch.from_numpy(V[b]).repeat_interleave(R, dim=0)
+        want = torch.nn.functional.scaled_dot_product_attention(qs[b], Kt, Vt, attn_mask=mask,
+                                                                scale=1.0).numpy()
+        np.testing.assert_allclose(got[b], want, atol=1e-9)
+    # (2) the kernel's score form over the packed fields
+    from scipy.linalg import hadamard
+
+    Hm = hadamard(d).astype(np.float64) / np.sqrt(d)
+    q_rot = (qs.numpy() * sg) @ Hm.T                     # R_K q_s = H (s * q) / sqrt(d)
+    q_proj = qs.numpy() @ P.astype(np.float64).T         # P q_s
+    sgn = O.unpack_lowbit(sbits, 1, d).astype(np.float64) * 2 - 1
+    c = mcb.astype(np.float64)[O.unpack_lowbit(mse, bits - 1, d)] if bits > 1 else 0.0 * sgn
+    n64, rn64 = n.astype(np.float64), rn.astype(np.float64)
+    b, e = 0, lengths[0]
+    for h in range(Hq):
+        g = h // R
+        sc = n64[b, g][None, :] * (q_rot[b, h] @ c[b, g].T) + \
+            n64[b, g][None, :] * rn64[b, g][None, :] * float(O.prod_scale(d)) * (q_proj[b, h] @ sgn[b, g].T)
+        qpos = e - L + np.arange(L)
+        sc = np.where(np.arange(T)[None, :] <= qpos[:, None], sc, -np.inf)
+        p = np.exp(sc - sc.max(axis=-1, keepdims=True))
+        o = (p @ V[b, g]) / p.sum(axis=-1, keepdims=True)
+        np.testing.assert_allclose(got[b, h], o, atol=1e-9)
