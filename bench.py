@@ -557,7 +557,7 @@ def main():
                      "traffic": CFG1_TRAFFIC_BYTES,
                      "traffic_note": "HBM bytes per call from rocprofv3 FETCH_SIZE/WRITE_SIZE, "
                                      "copy-calibrated; algorithmic bytes are 27,262,976",
-                     "kernel": "attention call: attn_small_kernel<128,3,3> + attn_merge_kernel<128>",
+                     "kernel": "attention call: attn_stage_kernel<128,3,3> + attn_merge_rot_kernel<128>",
                      "call_us": round(dec["ms_per_step"] * 1e3, 3),
                      "achieved_note": "algorithmic bytes / time of one whole attention call (both "
                                       "kernels, HIP events around a graph replay); the per-kernel "

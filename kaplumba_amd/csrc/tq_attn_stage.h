@@ -19,11 +19,14 @@
 // Lane roles (l = lane, n = l % 16, g = l / 16), as in attn_small_kernel:
 //   scores  S^T[tok][col] = sum_d k[tok][d] * q_col[d]    (16 x 16 tile, 32 tokens)
 //     A = keys: lane (m, g) holds token 16 (g >> 1) + m, coordinate half
-//         g & 1, eight coordinates per MFMA: the hi parts of a pair-table
-//         entry in one MFMA, the lo parts in the next,
+//         g & 1, four coordinates per MFMA as two pair-table entries read
+//         straight into the operand: k slots (hi c0, hi c1, lo c0, lo c1,
+//         hi c2, hi c3, lo c2, lo c3),
 //     B = queries: column n = 8p + 4j + r is piece p (hi / lo) of query row r
 //         for token subset j (zero where the lane group holds the other
-//         subset); one DPP row rotation by 8 adds the pieces.
+//         subset), each coordinate pair twice against the hi and lo slots;
+//         held in registers for the whole loop; one DPP row rotation by 8
+//         adds the pieces.
 //   softmax per lane: 4 tokens of one row, lazy reference maximum.
 //   values  O[row][d] = sum_tok w[row][tok] * v[tok][d]      (16 x 16 tiles)
 //     A = weights (f16, own four tokens and those of lane n + 4 by DPP),
@@ -60,7 +63,6 @@ struct StageShape {
   static constexpr int KW = HALF * KB / 32;  // key words per lane (half a row)
   static constexpr int PWK = D * KB / 32;
   static constexpr int PWV = D * VB / 32;
-  static constexpr int NKI = D / 16;  // MFMA steps per key piece (8 coordinates each)
   static constexpr int KKEYS = 1 << (2 * KB);
   static constexpr int VKEYS = 1 << (2 * VB);
   static constexpr int REPK = KKEYS <= 64 ? 32 : 16;
@@ -83,7 +85,7 @@ struct StageShape {
   static constexpr int LUTK_OFF = 0;
   static constexpr int LUTV_OFF = KTAB;
   static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [p][r][h][i] 8 x f16 = 16 B
-  static constexpr int QST_BYTES = 2 * NQ * 2 * NKI * 16;
+  static constexpr int QST_BYTES = 2 * NQ * 2 * (D / 8) * 16;
   static constexpr int ZERO_OFF = QST_OFF + QST_BYTES;
   static constexpr int QY_OFF = ZERO_OFF + 16;  // [NQ][D] f32
   static constexpr int QMAX_OFF = QY_OFF + NQ * D * 4;
@@ -195,7 +197,6 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   constexpr int SUB = S::SUB;
   constexpr int NQ = S::NQ;
   constexpr int KW = S::KW;
-  constexpr int NKI = S::NKI;
   constexpr int CPL = S::CPL;
   constexpr int VRAW = S::VRAW;
   constexpr int PWK = S::PWK;
@@ -380,8 +381,9 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     if (lane == 0) reinterpret_cast<float*>(lds + S::QMAX_OFF)[wave] = m;
   }
   lds_only_barrier();
-  // query pieces in B-operand order: staging [p][r][h][i] holds
-  // q_p,r[h D/2 + 8 i + e], e = 0..7, as f16 (one hi/lo scale for all rows)
+  // query pieces in B-operand order: staging [p][r][h][jj] holds, as f16
+  // pairs, (q01, q01, q23, q23) of coordinates h D/2 + 4 jj + 0..3 of piece p
+  // of row r (one hi/lo scale for all rows)
   const float* qmaxs = reinterpret_cast<const float*>(lds + S::QMAX_OFF);
   const float sq = f16_split_scale(fmaxf(fmaxf(qmaxs[0], qmaxs[1]), fmaxf(qmaxs[2], qmaxs[3])));
   for (int idx = tid; idx < NQ * D / 2; idx += NT) {
@@ -392,11 +394,14 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     split_f16(qq.x * sq, hi0, lo0);
     split_f16(qq.y * sq, hi1, lo1);
     const int h = c / (D / 2);
-    const int i = (c % (D / 2)) / 8;
-    const int e = c % 8;
+    const int jj = (c % (D / 2)) / 4;   // 4-coordinate group
+    const int e = (c % 4) / 2;          // pair within the group
     uint32_t* st = reinterpret_cast<uint32_t*>(lds + S::QST_OFF);
-    st[((((0 * NQ + r) * 2 + h) * NKI + i) * 8 + e) / 2] = hi0 | (hi1 << 16);
-    st[((((1 * NQ + r) * 2 + h) * NKI + i) * 8 + e) / 2] = lo0 | (lo1 << 16);
+    // [p][r][h][jj] = (pair0, pair0, pair1, pair1)
+    const int base0 = (((0 * NQ + r) * 2 + h) * (D / 8) + jj) * 4 + 2 * e;
+    const int base1 = (((1 * NQ + r) * 2 + h) * (D / 8) + jj) * 4 + 2 * e;
+    st[base0] = st[base0 + 1] = hi0 | (hi1 << 16);
+    st[base1] = st[base1 + 1] = lo0 | (lo1 << 16);
   }
   lds_only_barrier();
 
@@ -404,11 +409,16 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   const int jq = (n >> 2) & 1;  // token subset of this lane's score column
   const int rq = n & 3;         // query row of this lane's score column
   // B operands of lane (column n = 8 p + 4 jq + rq, g): zero unless lane
-  // group g holds tokens of subset jq; read from LDS per MFMA step
-  const uint32_t qb_addr = ((g >> 1) == jq)
-                               ? static_cast<uint32_t>(S::QST_OFF + ((((n >> 3) * NQ + rq) * 2 + (g & 1)) * NKI) * 16)
-                               : static_cast<uint32_t>(S::ZERO_OFF);
-  const uint32_t qb_step = ((g >> 1) == jq) ? 16u : 0u;
+  // group g holds tokens of subset jq
+  u32x4_t qd[D / 8];
+  {
+    const uint32_t qb_addr = ((g >> 1) == jq)
+                                 ? static_cast<uint32_t>(S::QST_OFF + ((((n >> 3) * NQ + rq) * 2 + (g & 1)) * (D / 8)) * 16)
+                                 : static_cast<uint32_t>(S::ZERO_OFF);
+    const uint32_t qb_step = ((g >> 1) == jq) ? 16u : 0u;
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) qd[j] = lds_at<u32x4_t>(lds, qb_addr + j * qb_step);
+  }
   // keys: token 16 (g >> 1) + n, half g & 1 of the slot's rows
   const uint32_t k_lane = (16 * (g >> 1) + n) * (PWK * 4) + (g & 1) * (KW * 4);
   // norms: tokens 16 jq + 4 g .. + 3 of the sub-chunk
@@ -513,21 +523,17 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     stage(slot, sub_start(i + NS));
     slot = slot + 1 == NS ? 0 : slot + 1;
 
-    // ---- scores: two chains (key hi parts, key lo parts) over NKI steps
+    // ---- scores: D / 8 MFMAs in two alternating accumulator chains
     f32x4_t Ch = {0.f, 0.f, 0.f, 0.f}, Cl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < NKI; ++st) {
-      u32x4_t ah, al;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t a = key_addr<2 * KB, S::LOGSK>(kw, (8 * st + 2 * u) * KB, lutk_lane, kmask);
-        const uint2 ent = lds_at<uint2>(lds, S::LUTK_OFF + a);
-        ah[u] = ent.x;
-        al[u] = ent.y;
-      }
-      const u32x4_t qb = lds_at<u32x4_t>(lds, qb_addr + st * qb_step);
-      Ch = mfma_f16(ah, qb, Ch);
-      Cl = mfma_f16(al, qb, Cl);
+    for (int j = 0; j < D / 8; ++j) {
+      const uint2 e0 = lds_at<uint2>(lds, S::LUTK_OFF + key_addr<2 * KB, S::LOGSK>(kw, (4 * j) * KB, lutk_lane, kmask));
+      const uint2 e1 = lds_at<uint2>(lds, S::LUTK_OFF + key_addr<2 * KB, S::LOGSK>(kw, (4 * j + 2) * KB, lutk_lane, kmask));
+      const u32x4_t a = {e0.x, e0.y, e1.x, e1.y};
+      if (j & 1)
+        Cl = mfma_f16(a, qd[j], Cl);
+      else
+        Ch = mfma_f16(a, qd[j], Ch);
     }
     const f32x4_t C = Ch + Cl;
 
