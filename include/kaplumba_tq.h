@@ -44,6 +44,10 @@ enum {
 enum { TQ_DTYPE_F32 = 0, TQ_DTYPE_F16 = 1, TQ_DTYPE_BF16 = 2 };
 enum { TQ_ROT_HADAMARD = 0, TQ_ROT_DENSE = 1 };
 enum { TQ_KV_PACKED = 0, TQ_KV_PLAIN = 1, TQ_KV_PROD = 2 /* tq_attention_prod keys */ };
+/* Array attention masks (tq_attention_general): boolean (uint8, nonzero keeps
+ * the score) or additive in f32 / f16 / bf16. */
+enum { TQ_MASK_NONE = 0, TQ_MASK_BOOL = 1, TQ_MASK_ADD_F32 = 2, TQ_MASK_ADD_F16 = 3,
+       TQ_MASK_ADD_BF16 = 4 };
 
 /* Library version string, e.g. "kaplumba_tq 0.1.0 gfx950". */
 const char* tq_version(void);
@@ -183,7 +187,9 @@ int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
  * seq_lens: NULL (every sequence holds max_tokens tokens) or a device int32
  *   array of B lengths, each <= max_tokens (ragged batches).
  * q: [B, Hq, L, dim] with element strides; out: contiguous [B, Hq, L, dim].
- * dim in {64, 128, 256}; L >= 1; Hq % Hkv == 0.
+ * dim: multiples of 8 in 8..512 (powers of two for the Hadamard rotation);
+ * 64 / 128 / 256 run the tuned kernels, other dims the kernels of
+ * tq_attention_general.  L >= 1; Hq % Hkv == 0.
  * workspace: >= tq_attention_workspace_size() bytes, 256-byte aligned, no
  *   initial contents needed (a call overwrites what it reads).  Calls that
  *   may run concurrently (other streams) must use different workspaces.
@@ -232,9 +238,11 @@ int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int 
  *   s_t = n_t (R_K q_s) . c[idx_t] + n_t rn_t sqrt(pi/2)/dim (q_s @ P^T) . sgn_t
  * with sgn = +-1 from the sign bits; softmax, value sum, R_V^-1 and the
  * causal / ragged / left-padding rules as tq_attention_ranged.
- * k_bits is the Prod width (2..4; the MSE part k_mse has k_bits - 1 bits).
- * Built for dim 64 / 128 and at most 4 query rows per kv head (Hq/Hkv * L);
- * other shapes return TQ_ERR_UNSUPPORTED.  Workspace as tq_attention.
+ * k_bits is the Prod width (1..4; the MSE part k_mse has k_bits - 1 bits and
+ * is not read for k_bits == 1).  Dim 64 / 128 with at most 4 query rows per kv
+ * head (Hq/Hkv * L) and k_bits >= 2 run the fused row-group kernel; every
+ * other shape (power-of-two dims 32..512) runs the kernels of
+ * tq_attention_general.  Workspace as tq_attention.
  */
 int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
                       int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
@@ -261,6 +269,55 @@ int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
  * scratch byte it reads.  Every other argument and the results are those of
  * tq_attention_ranged.
  */
+/*
+ * Bytes of workspace tq_attention_general() needs (rotated and projected
+ * queries, split partials).
+ */
+int64_t tq_attention_general_workspace_size(int B, int Hq, int Hkv, int L, int k_dim, int v_dim,
+                                            int64_t max_tokens);
+
+/*
+ * Attention with the full generality of quantized_attention (tq.py:5110-5203):
+ *   - key and value head dims chosen independently (k_dim, v_dim: multiples of
+ *     8 in 8..512); q is [B, Hq, L, k_dim], out is contiguous
+ *     [B, Hq, L, v_dim] in q_dtype (the output takes value_codec.dim, :5131);
+ *   - a rotation kind per side (k_rot_kind, v_rot_kind; Hadamard needs a
+ *     power-of-two dim), as each _TurboQuantMSECodec picks its own (:4122-4139);
+ *   - kv_kind TQ_KV_PACKED (MSE keys, k_bits 1..4), TQ_KV_PROD (Prod keys of
+ *     width k_bits 1..4: k is the MSE part at k_bits - 1 bits, k_signs /
+ *     k_residual_norms / projection as tq_attention_prod, Hadamard keys) or
+ *     TQ_KV_PLAIN (k / v [B, Hkv, capacity, dim] in kv_dtype F16/BF16; norms,
+ *     codebooks and rotations ignored);
+ *   - an optional array mask, applied as _apply_attention_mask
+ *     (tq.py:5079-5108): the score of query row (b, head h = g*R + r,
+ *     position l) for cache row t (absolute, left padding included) reads
+ *       mask[b*s[0] + g*s[1] + r*s[2] + l*s[3] + t*s[4]]   (s = mask_strides,
+ *     5 element strides, 0 along broadcast axes; R = Hq / Hkv);
+ *     TQ_MASK_BOOL keeps the score where nonzero and sets -FLT_MAX elsewhere,
+ *     TQ_MASK_ADD_* adds the value to the f32 score.  This is the reference's
+ *     broadcast of a mask over the grouped scores (B, Hkv, R, L, T) (a 4-D
+ *     (B, H, L, T) mask gets its repeat axis inserted at position 2).
+ *     A row whose every score is -inf (additive -inf masks) gets a zero output.
+ *     mask_kind TQ_MASK_NONE ignores mask / mask_strides;
+ *   - causal, seq_starts, seq_lens as tq_attention_ranged; a mask and the
+ *     causal rule may be combined.
+ * Replaces the array-mask paths of quantized_attention and decode_attention
+ * (tq.py:5949-5992) and the array-mask SDPA of the fp16 layers
+ * (base.py:218-226).  The tuned entry points route here by themselves for
+ * shapes outside their kernels.
+ */
+int tq_attention_general(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int k_dim,
+                         int v_dim, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l,
+                         float scale, int kv_kind, int kv_dtype,
+                         const void* k, const void* k_norms, const void* k_signs,
+                         const void* k_residual_norms, int k_bits, const float* k_codebook,
+                         int k_rot_kind, const float* k_rot, const float* projection,
+                         const void* v, const void* v_norms, int v_bits, const float* v_codebook,
+                         int v_rot_kind, const float* v_rot, int norm_dtype, int64_t capacity,
+                         int64_t max_tokens, const int32_t* seq_starts, const int32_t* seq_lens,
+                         int causal, const void* mask, int mask_kind, const int64_t* mask_strides,
+                         void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 #define TQ_NOALLOC_SCRATCH_BYTES (16ll << 20)
 int tq_attention_noalloc(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
                          int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,

@@ -24,7 +24,8 @@ TQ_ERR_HIP = 4
 
 TQ_DTYPE_F32, TQ_DTYPE_F16, TQ_DTYPE_BF16 = 0, 1, 2
 TQ_ROT_HADAMARD, TQ_ROT_DENSE = 0, 1
-TQ_KV_PACKED, TQ_KV_PLAIN = 0, 1
+TQ_KV_PACKED, TQ_KV_PLAIN, TQ_KV_PROD = 0, 1, 2
+TQ_MASK_NONE, TQ_MASK_BOOL, TQ_MASK_ADD_F32, TQ_MASK_ADD_F16, TQ_MASK_ADD_BF16 = 0, 1, 2, 3, 4
 
 # name -> (restype, argtypes); the single source of truth for the exported set.
 SIGNATURES = {
@@ -100,6 +101,18 @@ SIGNATURES = {
         c_int, c_void_p, c_void_p,
         c_int64, c_int64, c_void_p, c_void_p, c_int,           # ..., seq_starts, seq_lens, causal
         c_void_p, c_void_p]),                                  # out, stream (static scratch)
+    "tq_attention_general_workspace_size": (c_int64, [c_int, c_int, c_int, c_int, c_int, c_int,
+                                                      c_int64]),
+    "tq_attention_general": (c_int, [
+        c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int,  # q, dtype, B, Hq, Hkv, L, k_dim, v_dim
+        c_int64, c_int64, c_int64, c_float,                    # q strides, scale
+        c_int, c_int,                                          # kv_kind, kv_dtype
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,         # k, k_norms, k_signs, k_rnorms, k_bits
+        c_void_p, c_int, c_void_p, c_void_p,                   # k codebook, k_rot_kind, k_rot, projection
+        c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p,  # v, v_norms, v_bits, v codebook, v_rot_kind, v_rot
+        c_int, c_int64, c_int64, c_void_p, c_void_p, c_int,    # norm dtype, cap, T, starts, lens, causal
+        c_void_p, c_int, c_void_p,                             # mask, mask_kind, mask_strides (5 x int64)
+        c_void_p, c_void_p, c_int64, c_void_p]),               # out, workspace, ws bytes, stream
 }
 
 # Scratch bytes of tq_attention_noalloc (TQ_NOALLOC_SCRATCH_BYTES in the header).

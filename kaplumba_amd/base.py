@@ -12,7 +12,7 @@ import torch
 
 from . import ops
 from .batch_cache import BatchKVCache
-from .cache import _mask_is_causal
+from .cache import _split_mask
 
 
 def scaled_dot_product_attention(queries: torch.Tensor, keys, values, cache, scale: float,
@@ -33,6 +33,6 @@ def scaled_dot_product_attention(queries: torch.Tensor, keys, values, cache, sca
                                        scale=scale, mask=mask)
     if sinks is not None:
         raise NotImplementedError("attention sinks are not supported by the HIP kernels")
-    causal = _mask_is_causal(mask, queries.shape[-2])
+    causal, arr = _split_mask(mask, queries.shape[-2])
     starts = cache._seq_starts(queries.device) if isinstance(cache, BatchKVCache) else None
-    return ops.attention_plain(queries, keys, values, scale, causal, seq_starts=starts)
+    return ops.attention_plain(queries, keys, values, scale, causal, seq_starts=starts, mask=arr)

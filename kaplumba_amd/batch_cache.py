@@ -31,7 +31,7 @@ import torch
 
 from . import ops
 from .cache import (KVCache, TurboQuantKVCache, TurboQuantMSEState, _BaseCache,
-                    _codec_meta_fields, _mask_is_causal, _parse_codec_meta_fields,
+                    _codec_meta_fields, _split_mask, _parse_codec_meta_fields,
                     _QuantizedStateProxy, _unwrap, _validate_bits, create_causal_mask)
 from .codebook import DEFAULT_TURBOQUANT_SEED
 
@@ -274,10 +274,10 @@ class BatchTurboQuantKVCache(_LeftPadded, _BaseCache):
     def _attend(self, queries, keys_state, values_state, scale, mask):
         ks, vs = self._states(keys_state, values_state)
         self._codecs_ready()
-        causal = _mask_is_causal(mask, queries.shape[-2])
+        causal, arr = _split_mask(mask, queries.shape[-2])
         return ops.attention_packed(queries, ks.norms, ks.indices, vs.norms, vs.indices,
                                     self.key_codec, self.value_codec, scale, causal,
-                                    seq_starts=self._seq_starts(queries.device))
+                                    seq_starts=self._seq_starts(queries.device), mask=arr)
 
     def decode_attention(self, queries, keys_state=None, values_state=None, scale: float = 1.0,
                          mask=None):

@@ -115,17 +115,20 @@ def _parse_codec_meta_fields(extra) -> Dict[str, Any]:
     return opts
 
 
-def _mask_is_causal(mask, n_queries: int) -> bool:
-    """None / "causal" masks; other masks are rejected (array masks are not built)."""
+def _split_mask(mask, n_queries: int):
+    """(causal, array mask or None) of an attention mask argument.
+
+    None, ``"causal"`` (meaningful for more than one query) or an array
+    (boolean keep-mask or additive), as ``_apply_attention_mask`` accepts
+    (turboquant_cache.py:5079-5108); other strings are rejected there too.
+    """
     if mask is None:
-        return False
+        return False, None
     if isinstance(mask, str):
         if mask == "causal":
-            return n_queries > 1
+            return n_queries > 1, None
         raise ValueError(f"Unsupported TurboQuant attention mask: {mask}")
-    raise NotImplementedError(
-        "array attention masks are not supported by the HIP attention kernels; "
-        "pass None or 'causal'")
+    return False, mask
 
 
 class _BaseCache:
@@ -352,12 +355,12 @@ class TurboQuantKVCache(_BaseCache):
     def _attend(self, queries, keys_state, values_state, scale, mask):
         ks, vs = self._states(keys_state, values_state)
         self._ensure_codecs_from_meta()
-        causal = _mask_is_causal(mask, queries.shape[-2])
+        causal, arr = _split_mask(mask, queries.shape[-2])
         if isinstance(self.key_codec, ProdCodec):
             return attention_prod(queries, ks, vs.norms, vs.indices, self.key_codec,
-                                  self.value_codec, scale, causal)
+                                  self.value_codec, scale, causal, mask=arr)
         return ops.attention_packed(queries, ks.norms, ks.indices, vs.norms, vs.indices,
-                                    self.key_codec, self.value_codec, scale, causal)
+                                    self.key_codec, self.value_codec, scale, causal, mask=arr)
 
     def decode_attention(self, queries, keys_state=None, values_state=None, scale: float = 1.0,
                          mask=None):

@@ -4,6 +4,7 @@
 #include <cstdlib>
 #include <mutex>
 
+#include "tq_attn_general.h"
 #include "tq_attn_splitmerge.h"
 
 namespace tq {
@@ -191,10 +192,13 @@ extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, in
                                                int64_t max_tokens) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || dim <= 0 || max_tokens < 0 || Hq % Hkv)
     return 0;
-  // large enough for either cache kind
+  // large enough for either cache kind and for the general kernels, which
+  // serve the shapes outside the tuned ones
   const int64_t T = std::max<int64_t>(max_tokens, 1);
-  return std::max(workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, true), B, Hq, Hkv, L, dim),
-                  workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, false), B, Hq, Hkv, L, dim));
+  const int64_t tuned =
+      std::max(workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, true), B, Hq, Hkv, L, dim),
+               workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, false), B, Hq, Hkv, L, dim));
+  return std::max(tuned, general_workspace_bytes(B, Hq, Hkv, L, dim, dim, T, true));
 }
 
 namespace {
@@ -218,8 +222,54 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
                    const ProdKeys* prod) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || L < 1 || Hq % Hkv)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bad heads/L (Hq %d, Hkv %d, L %d)", Hq, Hkv, L);
-  if (dim != 64 && dim != 128 && dim != 256)
-    return fail(TQ_ERR_UNSUPPORTED, "attention: dim %d not in {64, 128, 256}", dim);
+  // Shapes outside the tuned kernels (other head dims; Prod keys beyond
+  // d <= 128 and 4 rows per kv head, or 1-bit Prod) run the general kernels.
+  const bool tuned_dim = dim == 64 || dim == 128 || dim == 256;
+  const bool prod_small = prod && dim <= 128 && static_cast<int64_t>(Hq / Hkv) * L <= 4 && k_bits >= 1;
+  if (!tuned_dim || (prod && !prod_small)) {
+    GenCall c{};
+    c.q = q;
+    c.q_dtype = q_dtype;
+    c.B = B;
+    c.Hq = Hq;
+    c.Hkv = Hkv;
+    c.L = L;
+    c.Dk = dim;
+    c.Dv = dim;
+    c.q_sb = q_stride_b;
+    c.q_sh = q_stride_h;
+    c.q_sl = q_stride_l;
+    c.scale = scale;
+    c.kv_kind = kv_kind;
+    c.kv_dtype = kv_dtype;
+    c.k = k;
+    c.k_norms = k_norms;
+    c.k_signs = prod ? prod->signs : nullptr;
+    c.k_rnorms = prod ? prod->rnorms : nullptr;
+    c.k_bits = prod ? k_bits + 1 : k_bits;  // the Prod width
+    c.k_codebook = k_codebook;
+    c.k_rot_kind = rot_kind;
+    c.k_rot = k_rot;
+    c.projection = prod ? prod->proj : nullptr;
+    c.v = v;
+    c.v_norms = v_norms;
+    c.v_bits = v_bits;
+    c.v_codebook = v_codebook;
+    c.v_rot_kind = rot_kind;
+    c.v_rot = v_rot;
+    c.norm_dtype = norm_dtype;
+    c.capacity = capacity;
+    c.max_tokens = max_tokens;
+    c.seq_starts = seq_starts;
+    c.seq_lens = seq_lens;
+    c.causal = causal;
+    c.mask_kind = TQ_MASK_NONE;
+    c.out = out;
+    c.workspace = workspace;
+    c.workspace_bytes = workspace_bytes_given;
+    c.stream = stream;
+    return general_attention(c);
+  }
   if (q_dtype != TQ_DTYPE_F32 && q_dtype != TQ_DTYPE_F16 && q_dtype != TQ_DTYPE_BF16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: q_dtype %d", q_dtype);
   if (capacity > INT32_MAX)
@@ -228,12 +278,9 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: max_tokens %lld > capacity %lld",
                 (long long)max_tokens, (long long)capacity);
   if (prod) {
-    // Prod keys: the small row-group kernel (<= 4 query rows per kv head, d <= 128)
-    if (dim > 128 || static_cast<int64_t>(Hq / Hkv) * L > 4)
-      return fail(TQ_ERR_UNSUPPORTED, "attention: Prod keys need d <= 128 and at most 4 query rows "
-                  "per kv head (got d %d, %d rows)", dim, (Hq / Hkv) * L);
-    if (k_bits < 1 || k_bits > 3)
-      return fail(TQ_ERR_UNSUPPORTED, "attention: Prod keys of %d bits (2..4 are built)", k_bits + 1);
+    // Prod keys here: the small row-group kernel (<= 4 query rows per kv head, d <= 128)
+    if (k_bits > 3)
+      return fail(TQ_ERR_INVALID_ARGUMENT, "attention: Prod keys of %d bits (1..4)", k_bits + 1);
     if (rot_kind != TQ_ROT_HADAMARD)
       return fail(TQ_ERR_INVALID_ARGUMENT, "attention: Prod keys use the Hadamard rotation");
     if (max_tokens > 0 && (!prod->signs || !prod->rnorms))

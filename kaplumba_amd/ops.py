@@ -6,6 +6,7 @@ there is no CPU path.
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass, field
 from typing import Dict, Optional
 
@@ -271,25 +272,102 @@ def _call_attention(lib, head, seq_starts, seq_lens, tail, what: str) -> None:
     _lib.check(rc, what)
 
 
+def prepare_mask(mask, B: int, Hkv: int, R: int, L: int, T: int, device, grouped: bool = True):
+    """An array mask as (tensor kept alive, mask kind, 5 element strides) over
+    the grouped scores (B, Hkv, R, L, T).
+
+    ``grouped`` follows ``_apply_attention_mask`` (turboquant_cache.py:5101-5104):
+    the mask is sliced ``[..., :L, :T]``, a 4-D mask gets its repeat axis
+    inserted at position 2, and the rest is broadcasting against
+    (B, Hkv, R, L, T).  Otherwise (the fp16 layers' SDPA, base.py:218-226) it
+    broadcasts against (B, Hq, L, T) and head h = g * R + r.  Boolean masks
+    keep a score where True; float masks are added.  Key index t is the cache
+    row (left padding included).
+    """
+    m = mask if isinstance(mask, torch.Tensor) else torch.as_tensor(np.asarray(mask))
+    m = m.to(device)
+    if m.dtype == torch.bool:
+        kind = _lib.TQ_MASK_BOOL
+    elif m.dtype == torch.float32:
+        kind = _lib.TQ_MASK_ADD_F32
+    elif m.dtype == torch.float16:
+        kind = _lib.TQ_MASK_ADD_F16
+    elif m.dtype == torch.bfloat16:
+        kind = _lib.TQ_MASK_ADD_BF16
+    else:
+        m, kind = m.to(torch.float32), _lib.TQ_MASK_ADD_F32
+    if m.dim() < 2:
+        raise ValueError(f"attention mask needs (..., queries, keys) axes, got shape {tuple(m.shape)}")
+    m = m[..., :L, :T]
+    try:
+        if grouped:
+            if m.dim() == 4:
+                m = m.unsqueeze(2)
+            if m.dim() > 5:
+                raise RuntimeError("more than 5 axes")
+            m = m.expand(B, Hkv, R, L, T)
+            strides = m.stride()
+        else:
+            if m.dim() > 4:
+                raise RuntimeError("more than 4 axes")
+            m = m.expand(B, Hkv * R, L, T)
+            sb, sh, sl, st = m.stride()
+            strides = (sb, R * sh, sh, sl, st)
+    except RuntimeError as e:
+        want = f"(B, Hkv, R, L, T) = {(B, Hkv, R, L, T)}" if grouped else f"(B, Hq, L, T) = {(B, Hkv * R, L, T)}"
+        raise ValueError(f"attention mask of shape {tuple(mask.shape)} does not broadcast to {want}: {e}")
+    st5 = (ctypes.c_int64 * 5)(*strides)
+    return m, kind, st5
+
+
+def _attention_general(queries: torch.Tensor, *, Dv: int, kv_kind: int, kv_dtype: int, k, k_norms,
+                       k_signs, k_rnorms, k_bits: int, k_codebook, k_rot_kind: int, k_rot,
+                       projection, v, v_norms, v_bits: int, v_codebook, v_rot_kind: int, v_rot,
+                       norm_dtype: int, cap: int, T: int, scale: float, causal: bool, mask,
+                       seq_lens, seq_starts, grouped_mask: bool = True) -> torch.Tensor:
+    """One tq_attention_general call (pointers may be None where unused)."""
+    B, Hq, L, Dk = queries.shape
+    Hkv = (k_norms if k_norms is not None else k).shape[1]
+    R = Hq // Hkv
+    mt, mkind, mstr = (None, _lib.TQ_MASK_NONE, None)
+    if mask is not None:
+        mt, mkind, mstr = prepare_mask(mask, B, Hkv, R, L, T, queries.device, grouped_mask)
+    out = torch.empty((B, Hq, L, Dv), dtype=queries.dtype, device=queries.device)
+    lib = _lib.load()
+    ws = _workspace(queries.device, lib.tq_attention_general_workspace_size(B, Hq, Hkv, L, Dk, Dv, T))
+
+    def ptr(t):
+        return t.data_ptr() if t is not None else None
+
+    rc = lib.tq_attention_general(
+        queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, Dk, Dv,
+        queries.stride(0), queries.stride(1), queries.stride(2), float(scale), kv_kind, kv_dtype,
+        ptr(k), ptr(k_norms), ptr(k_signs), ptr(k_rnorms), k_bits, ptr(k_codebook), k_rot_kind,
+        ptr(k_rot), ptr(projection), ptr(v), ptr(v_norms), v_bits, ptr(v_codebook), v_rot_kind,
+        ptr(v_rot), norm_dtype, cap, T, ptr(seq_starts), ptr(seq_lens), 1 if causal else 0,
+        ptr(mt), mkind, mstr, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
+    _lib.check(rc, "tq_attention_general")
+    return out
+
+
 def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.Tensor,
                      v_norms: torch.Tensor, v_idx: torch.Tensor, key_codec: Codec,
                      value_codec: Codec, scale: float, causal: bool,
                      seq_lens: Optional[torch.Tensor] = None,
-                     seq_starts: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     seq_starts: Optional[torch.Tensor] = None, mask=None) -> torch.Tensor:
     """Attention straight from packed K/V state views (B, Hkv, T[, PW]).
 
     ``seq_lens`` (B,) ends each sequence before T (ragged batches);
-    ``seq_starts`` (B,) skips each sequence's left padding.
+    ``seq_starts`` (B,) skips each sequence's left padding; ``mask`` is an
+    optional array mask (``prepare_mask``).  Key and value codecs may differ
+    in head dim and rotation; the output has the value dim
+    (turboquant_cache.py:5131).
     """
     _require_device(queries, k_norms, k_idx, v_norms, v_idx)
     B, Hq, L, D = queries.shape
     Hkv, T = k_norms.shape[1], k_norms.shape[2]
-    if key_codec.dim != D or value_codec.dim != D:
-        raise NotImplementedError(
-            f"attention with key dim {key_codec.dim} / value dim {value_codec.dim} "
-            f"and query dim {D}: only equal K/V head dims are built")
-    if key_codec.rotation != value_codec.rotation:
-        raise NotImplementedError("K and V codecs must use the same rotation kind")
+    if key_codec.dim != D:
+        raise ValueError(f"query head dim {D} != key codec dim {key_codec.dim}")
     if Hq % Hkv:
         raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} kv heads")
     if queries.stride(-1) != 1:
@@ -302,12 +380,21 @@ def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.
         raise ValueError("key and value norms must share a dtype")
     seq_lens = _seq_array(seq_lens, B, queries.device)
     seq_starts = _seq_array(seq_starts, B, queries.device)
+    kt = key_codec.device_tensors(queries.device)
+    vt = value_codec.device_tensors(queries.device)
+    if (mask is not None or value_codec.dim != D or key_codec.rotation != value_codec.rotation):
+        return _attention_general(
+            queries, Dv=value_codec.dim, kv_kind=_lib.TQ_KV_PACKED, kv_dtype=0, k=k_idx,
+            k_norms=k_norms, k_signs=None, k_rnorms=None, k_bits=key_codec.bits,
+            k_codebook=kt["codebook"], k_rot_kind=key_codec.rot_kind, k_rot=kt["rot"],
+            projection=None, v=v_idx, v_norms=v_norms, v_bits=value_codec.bits,
+            v_codebook=vt["codebook"], v_rot_kind=value_codec.rot_kind, v_rot=vt["rot"],
+            norm_dtype=_lib.torch_dtype_code(k_norms.dtype), cap=cap, T=T, scale=scale,
+            causal=causal, mask=mask, seq_lens=seq_lens, seq_starts=seq_starts)
     out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
     lib = _lib.load()
     wsb = lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T)
     ws = _workspace(queries.device, wsb)
-    kt = key_codec.device_tensors(queries.device)
-    vt = value_codec.device_tensors(queries.device)
     head = (queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
             queries.stride(0), queries.stride(1), queries.stride(2), float(scale),
             _lib.TQ_KV_PACKED, 0,
@@ -320,38 +407,60 @@ def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.
     return out
 
 
+def _plain_capacity(t: torch.Tensor) -> int:
+    """Token capacity of a (B, H, T, D) view of a contiguous (B, H, cap, D) buffer."""
+    B, H, T, D = t.shape
+    if t.stride(3) != 1 or (T > 1 and t.stride(2) != D):
+        raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
+    if H > 1:
+        cap = t.stride(1) // D
+    elif B > 1:
+        cap = t.stride(0) // D
+    else:
+        cap = max(T, 1)
+    if (H > 1 and t.stride(1) != cap * D) or (B > 1 and t.stride(0) != H * cap * D) or cap < T:
+        raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
+    return cap
+
+
 def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                     scale: float, causal: bool,
                     seq_lens: Optional[torch.Tensor] = None,
-                    seq_starts: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Attention over unquantized fp16/bf16 K/V views (B, Hkv, T, D) of (B, Hkv, cap, D).
+                    seq_starts: Optional[torch.Tensor] = None, mask=None) -> torch.Tensor:
+    """Attention over unquantized fp16/bf16 K/V views (B, Hkv, T, Dk / Dv) of
+    (B, Hkv, cap, D) buffers.
 
-    ``seq_lens`` / ``seq_starts`` as in ``attention_packed``.
+    ``seq_lens`` / ``seq_starts`` as in ``attention_packed``; ``mask`` is an
+    array mask broadcast as the fp16 layers' SDPA does (against
+    (B, Hq, L, T), base.py:218-226).
     """
     _require_device(queries, keys, values)
     B, Hq, L, D = queries.shape
     Hkv, T = keys.shape[1], keys.shape[2]
+    Dv = values.shape[-1]
     if keys.dtype != values.dtype or keys.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("plain K/V must both be float16 or bfloat16")
-    if keys.shape[-1] != D or values.shape[-1] != D:
-        raise NotImplementedError("only equal query/key/value head dims are built")
+    if keys.shape[-1] != D:
+        raise ValueError(f"query head dim {D} != key head dim {keys.shape[-1]}")
+    if values.shape[:3] != keys.shape[:3]:
+        raise ValueError("plain keys and values must share (B, H, T)")
     if Hq % Hkv:
         raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} kv heads")
-    for t in (keys, values):
-        if t.stride(3) != 1 or t.stride(2) != D:
-            raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
-    if Hkv > 1:
-        cap = keys.stride(1) // D
-    elif B > 1:
-        cap = keys.stride(0) // D
-    else:
-        cap = max(T, 1)
-    if keys.stride() != values.stride() or (B > 1 and keys.stride(0) != Hkv * cap * D):
-        raise ValueError("plain K/V views must slice contiguous (B, H, cap, D) buffers")
+    cap = _plain_capacity(keys)
+    if _plain_capacity(values) != cap:
+        raise ValueError("plain keys and values must share a capacity")
     if queries.stride(-1) != 1:
         queries = queries.contiguous()
     seq_lens = _seq_array(seq_lens, B, queries.device)
     seq_starts = _seq_array(seq_starts, B, queries.device)
+    if mask is not None or Dv != D:
+        return _attention_general(
+            queries, Dv=Dv, kv_kind=_lib.TQ_KV_PLAIN, kv_dtype=_lib.torch_dtype_code(keys.dtype),
+            k=keys, k_norms=None, k_signs=None, k_rnorms=None, k_bits=0, k_codebook=None,
+            k_rot_kind=0, k_rot=None, projection=None, v=values, v_norms=None, v_bits=0,
+            v_codebook=None, v_rot_kind=0, v_rot=None, norm_dtype=0, cap=cap, T=T, scale=scale,
+            causal=causal, mask=mask, seq_lens=seq_lens, seq_starts=seq_starts,
+            grouped_mask=False)
     out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
     lib = _lib.load()
     wsb = lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T)

@@ -20,7 +20,8 @@ import torch
 
 from . import _lib
 from . import codebook as cbmod
-from .ops import (Codec, _capacity_of, _require_device, _seq_array, _stream, _workspace)
+from .ops import (Codec, _attention_general, _capacity_of, _require_device, _seq_array, _stream,
+                  _workspace)
 
 __all__ = ["ProdCodec", "TurboQuantProdState", "attention_prod"]
 
@@ -133,18 +134,18 @@ class ProdCodec:
 def attention_prod(queries: torch.Tensor, keys: TurboQuantProdState, v_norms: torch.Tensor,
                    v_idx: torch.Tensor, key_codec: ProdCodec, value_codec: Codec, scale: float,
                    causal: bool, seq_lens: Optional[torch.Tensor] = None,
-                   seq_starts: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   seq_starts: Optional[torch.Tensor] = None, mask=None) -> torch.Tensor:
     """Attention with Prod-coded keys and MSE-coded values (``tq_attention_prod``):
     the fused Prod decode kernel's scores (turboquant_cache.py:2000-2206) with
     ``quantized_attention``'s softmax and masks.  Views (B, Hkv, T[, W]) of
-    contiguous capacity buffers, as the cache hands them out."""
+    contiguous capacity buffers, as the cache hands them out.  ``mask`` is an
+    optional array mask (``ops.prepare_mask``); a value codec of another dim or
+    rotation, or a mask, runs ``tq_attention_general``."""
     _require_device(queries, *keys, v_norms, v_idx)
     B, Hq, L, D = queries.shape
     Hkv, T = keys.norms.shape[1], keys.norms.shape[2]
-    if key_codec.dim != D or value_codec.dim != D:
-        raise NotImplementedError("Prod attention needs equal query, key and value head dims")
-    if value_codec.rotation != "hadamard":
-        raise NotImplementedError("Prod attention pairs with Hadamard-rotated values")
+    if key_codec.dim != D:
+        raise ValueError(f"query head dim {D} != key codec dim {key_codec.dim}")
     if Hq % Hkv:
         raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} kv heads")
     if queries.stride(-1) != 1:
@@ -160,10 +161,20 @@ def attention_prod(queries: torch.Tensor, keys: TurboQuantProdState, v_norms: to
         raise ValueError("key norms, residual norms and value norms must share a dtype")
     seq_lens = _seq_array(seq_lens, B, queries.device)
     seq_starts = _seq_array(seq_starts, B, queries.device)
+    kt, vt = key_codec.device_tensors(queries.device), value_codec.device_tensors(queries.device)
+    if mask is not None or value_codec.dim != D or value_codec.rotation != "hadamard":
+        return _attention_general(
+            queries, Dv=value_codec.dim, kv_kind=_lib.TQ_KV_PROD, kv_dtype=0,
+            k=keys.mse_indices if key_codec.mse_bits > 0 else None, k_norms=keys.norms,
+            k_signs=keys.qjl_signs, k_rnorms=keys.residual_norms, k_bits=key_codec.bits,
+            k_codebook=kt["codebook"], k_rot_kind=_lib.TQ_ROT_HADAMARD, k_rot=kt["signs"],
+            projection=kt["projection"], v=v_idx, v_norms=v_norms, v_bits=value_codec.bits,
+            v_codebook=vt["codebook"], v_rot_kind=value_codec.rot_kind, v_rot=vt["rot"],
+            norm_dtype=_lib.torch_dtype_code(v_norms.dtype), cap=cap, T=T, scale=scale,
+            causal=causal, mask=mask, seq_lens=seq_lens, seq_starts=seq_starts)
     out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
     lib = _lib.load()
     ws = _workspace(queries.device, lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T))
-    kt, vt = key_codec.device_tensors(queries.device), value_codec.device_tensors(queries.device)
     rc = lib.tq_attention_prod(
         queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
         queries.stride(0), queries.stride(1), queries.stride(2), float(scale),

@@ -224,12 +224,22 @@ def norm_f32(x: np.ndarray) -> np.ndarray:
     The kernel gives each lane ``LANE_ELEMS`` consecutive elements (fewer when
     D < 32).  A lane squares its elements and folds them with distances
     16, 8, 4, 2, 1; lanes are then combined pairwise (xor 1, xor 2, ...).
+    A dim that is not a power of two is zero-padded to the next power of two
+    (below 32) or to a power-of-two number of 32-element lanes: the padding
+    adds exact zeros, so the tree is the same for every dim.
     ``sqrt`` is IEEE (correctly rounded).  Reference: ``mx.linalg.norm`` on
     f32 (:4192, :4249); MLX's own order is parity unpinned.
     """
     xf = np.asarray(x, np.float32)
     lead = xf.shape[:-1]
     d = xf.shape[-1]
+    if d <= LANE_ELEMS:
+        dp = 1 << (d - 1).bit_length()
+    else:
+        dp = LANE_ELEMS << (-(-d // LANE_ELEMS) - 1).bit_length()
+    if dp != d:
+        xf = np.concatenate([xf, np.zeros((*lead, dp - d), np.float32)], axis=-1)
+        d = dp
     ce = min(LANE_ELEMS, d)
     nl = d // ce
     s = (xf * xf).reshape(*lead, nl, ce)
@@ -438,7 +448,8 @@ def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: n
                    k_mse_codebook: Optional[np.ndarray], proj: np.ndarray,
                    v_codebook: np.ndarray, v_rot: np.ndarray, scale: float, q_dtype: str,
                    causal: bool = False, lengths: Optional[Sequence[int]] = None,
-                   starts: Optional[Sequence[int]] = None) -> np.ndarray:
+                   starts: Optional[Sequence[int]] = None,
+                   mask: Optional[np.ndarray] = None) -> np.ndarray:
     """Attention with Prod-coded keys and MSE-coded values, float64.
 
     Scores follow ``score_prepared`` (:4700-4766) -- ``n * q_rot . c[idx] +
@@ -455,9 +466,11 @@ def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: n
     kd_all = prod_key_vectors(k_norms, k_mse, k_rnorms, k_signs, bits=k_bits, dim=D,
                               signs=k_signs_rot, mse_codebook=k_mse_codebook, proj=proj)
     vc = v_codebook.astype(np.float64)
-    out = np.zeros((B, Hq, L, D), np.float64)
+    Dv = np.asarray(v_rot).shape[0]
+    out = np.zeros((B, Hq, L, Dv), np.float64)
     fmin = float(np.finfo(np.float32).min)
     cap = kd_all.shape[2]
+    m5 = None if mask is None else mask_5d(mask, B, Hkv, R, L, cap)
     for b in range(B):
         end = cap if lengths is None else int(lengths[b])
         t0 = 0 if starts is None else min(int(starts[b]), end)
@@ -466,7 +479,7 @@ def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: n
             continue
         for g in range(Hkv):
             kd = kd_all[b, g, t0:end]
-            vidx = unpack_lowbit(v_packed[b, g, t0:end], v_bits, D)
+            vidx = unpack_lowbit(v_packed[b, g, t0:end], v_bits, Dv)
             vd = vc[vidx] * np.asarray(v_norms[b, g, t0:end], np.float64)[:, None]
             for r in range(R):
                 h = g * R + r
@@ -474,6 +487,8 @@ def attention_prod(q: np.ndarray, k_norms, k_mse, k_rnorms, k_signs, v_packed: n
                 if causal:
                     qi = (T - L) + np.arange(L)[:, None]
                     s = np.where(qi >= np.arange(T)[None, :], s, fmin)
+                if m5 is not None:
+                    s = apply_mask(s, m5[b, g, r, :, t0:end])
                 m = s.max(axis=-1, keepdims=True)
                 p = np.exp(s - m)
                 l = p.sum(axis=-1, keepdims=True)
@@ -494,13 +509,39 @@ def scale_queries(q: np.ndarray, scale: float, q_dtype: str) -> np.ndarray:
     return round_to_dtype(np.asarray(q, np.float32) * s, q_dtype)
 
 
+def mask_5d(mask: np.ndarray, B: int, Hkv: int, R: int, L: int, T: int) -> np.ndarray:
+    """An array mask broadcast to the scores' shape (B, Hkv, R, L, T).
+
+    ``_apply_attention_mask`` (:5079-5108) slices ``mask[..., q, k]`` and, when
+    the mask has one dimension fewer than the 5-D grouped scores (a 4-D
+    ``(B, H, L, T)`` mask), inserts the repeat axis at position 2, so its
+    head axis lines up with the kv heads; otherwise numpy broadcasting
+    aligns it from the right.
+    """
+    m = np.asarray(mask)
+    m = m[..., :L, :T]
+    if m.ndim == 4:
+        m = np.expand_dims(m, 2)
+    return np.broadcast_to(m, (B, Hkv, R, L, T))
+
+
+def apply_mask(s: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """Boolean masks keep scores where True (f32 min elsewhere); other masks
+    are added (:5104-5108)."""
+    if m.dtype == np.bool_:
+        return np.where(m, s, float(np.finfo(np.float32).min))
+    return s + m.astype(np.float64)
+
+
 def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
               v_packed: np.ndarray, v_norms: np.ndarray, *, k_bits: int, v_bits: int,
               k_codebook: np.ndarray, v_codebook: np.ndarray, rot_kind: str,
               k_rot: np.ndarray, v_rot: np.ndarray, scale: float, q_dtype: str,
               causal: bool = False, lengths: Optional[Sequence[int]] = None,
               v_dim: Optional[int] = None,
-              starts: Optional[Sequence[int]] = None) -> np.ndarray:
+              starts: Optional[Sequence[int]] = None,
+              mask: Optional[np.ndarray] = None,
+              v_rot_kind: Optional[str] = None) -> np.ndarray:
     """TurboQuant attention in float64, ``quantized_attention`` semantics.
 
     Restates :5110-5203 with ``_apply_attention_mask`` (:5079-5108) and the
@@ -514,13 +555,18 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
     either, which is the left-padding mask ``left_padding <= k`` of
     models/base.py:40-41 that BatchKVCache.make_mask applies
     (models/cache.py:1195-1198); the causal rule still counts from the end.
-    Returns float64 (B, Hq, L, Dv); callers round to the query dtype.
+    ``mask`` is an array mask over absolute key positions (``mask_5d``,
+    ``apply_mask``).  ``v_rot_kind`` (default ``rot_kind``) is the value
+    codec's own rotation kind: each codec picks Hadamard or dense from its own
+    dim (:4122-4139).  Returns float64 (B, Hq, L, Dv); callers round to the
+    query dtype.
     """
     B, Hq, L, D = q.shape
     Hkv = k_packed.shape[1]
     R = Hq // Hkv
     Dv = v_dim if v_dim is not None else D
     cap = k_packed.shape[2]
+    m5 = None if mask is None else mask_5d(mask, B, Hkv, R, L, cap)
     qs = scale_queries(q, scale, q_dtype).astype(np.float64)
     if rot_kind == "hadamard":
         qr = rht_forward_f64(qs, k_rot)
@@ -548,11 +594,13 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
                     qi = (T - L) + np.arange(L)[:, None]
                     kj = np.arange(T)[None, :]
                     s = np.where(qi >= kj, s, fmin)
+                if m5 is not None:
+                    s = apply_mask(s, m5[b, g, r, :, t0:end])
                 m = s.max(axis=-1, keepdims=True)
                 p = np.exp(s - m)
                 l = p.sum(axis=-1, keepdims=True)
                 o_rot = p @ vd                            # (L, Dv)
-                if rot_kind == "hadamard":
+                if (v_rot_kind or rot_kind) == "hadamard":
                     o = rht_inverse_f64(o_rot, v_rot)
                 else:
                     o = o_rot @ v_rot.astype(np.float64)
@@ -563,13 +611,17 @@ def attention(q: np.ndarray, k_packed: np.ndarray, k_norms: np.ndarray,
 def attention_plain(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float,
                     q_dtype: str, causal: bool = False,
                     lengths: Optional[Sequence[int]] = None,
-                    starts: Optional[Sequence[int]] = None) -> np.ndarray:
+                    starts: Optional[Sequence[int]] = None,
+                    mask: Optional[np.ndarray] = None) -> np.ndarray:
     """Standard SDPA over an unquantized (fp16/bf16) cache, float64.
 
     The mixed-precision layers of the reference keep model-dtype K/V and call
     ``mx.fast.scaled_dot_product_attention`` (models/base.py:218-226,
     models/cache.py:55-61).  Queries are scaled in their dtype as above;
-    ``lengths`` and ``starts`` as in ``attention``.
+    ``lengths`` and ``starts`` as in ``attention``.  An array ``mask``
+    broadcasts against the (B, Hq, L, T) scores, as the fast SDPA's does
+    (sliced ``[..., :L, :T]`` over absolute key positions; boolean keeps,
+    other dtypes add, as ``apply_mask``).
     """
     B, Hq, L, D = q.shape
     Hkv = k.shape[1]
@@ -577,6 +629,9 @@ def attention_plain(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float
     qs = scale_queries(q, scale, q_dtype).astype(np.float64)
     out = np.zeros((B, Hq, L, v.shape[-1]), np.float64)
     fmin = float(np.finfo(np.float32).min)
+    m4 = None
+    if mask is not None:
+        m4 = np.broadcast_to(np.asarray(mask)[..., :L, :k.shape[2]], (B, Hq, L, k.shape[2]))
     for b in range(B):
         end = k.shape[2] if lengths is None else int(lengths[b])
         t0 = 0 if starts is None else min(int(starts[b]), end)
@@ -589,6 +644,8 @@ def attention_plain(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float
             if causal:
                 qi = (T - L) + np.arange(L)[:, None]
                 s = np.where(qi >= np.arange(T)[None, :], s, fmin)
+            if m4 is not None:
+                s = apply_mask(s, m4[b, h, :, t0:end])
             m = s.max(axis=-1, keepdims=True)
             p = np.exp(s - m)
             out[b, h] = (p @ np.asarray(v[b, g, t0:end], np.float64)) / np.maximum(

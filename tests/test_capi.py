@@ -73,15 +73,59 @@ def test_append_rejects_capacity_overflow_and_nulls():
 
 def test_attention_rejects_unsupported_dim_and_bad_heads():
     lib = _lib.load()
-    args = [None, 2, 1, 32, 8, 1, 96, 0, 0, 0, 0.1, 0, 0, None, None, None, None, 0, 3, 3,
+    args = [None, 2, 1, 32, 8, 1, 1024, 0, 0, 0, 0.1, 0, 0, None, None, None, None, 0, 3, 3,
             None, None, 0, None, None, 16, 16, None, 0, None, None, 0, None]
     assert lib.tq_attention(*args) == _lib.TQ_ERR_UNSUPPORTED
+    args[6] = 96  # not a power of two: only the dense rotation
+    assert lib.tq_attention(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
+    assert b"power-of-two" in lib.tq_last_error()
     args[6] = 128
     args[4] = 7
     assert lib.tq_attention(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
     args[4] = 8
     args[18] = 5  # k_bits
     assert lib.tq_attention(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
+
+
+def _general_args(**kw):
+    """tq_attention_general arguments of a B = 0 call (validated, nothing launched)."""
+    a = dict(q=None, q_dtype=2, B=0, Hq=32, Hkv=8, L=1, k_dim=128, v_dim=64, sb=0, sh=0, sl=0,
+             scale=0.1, kv_kind=_lib.TQ_KV_PACKED, kv_dtype=0, k=None, kn=None, ks=None, krn=None,
+             k_bits=3, kcb=None, k_rot_kind=0, k_rot=None, proj=None, v=None, vn=None, v_bits=3,
+             vcb=None, v_rot_kind=1, v_rot=None, norm_dtype=0, cap=16, T=0, starts=None,
+             lens=None, causal=0, mask=None, mask_kind=0, mstrides=None, out=None, ws=None,
+             wsb=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_general_attention_validates_without_the_gpu():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(16)
+    ok = dict(kcb=fake, k_rot=fake, vcb=fake, v_rot=fake)
+    assert lib.tq_attention_general(*_general_args(**ok)) == _lib.TQ_OK  # B = 0
+    bad = [
+        (dict(k_dim=520), _lib.TQ_ERR_UNSUPPORTED, b"head dims"),
+        (dict(v_dim=100), _lib.TQ_ERR_UNSUPPORTED, b"head dims"),
+        (dict(k_dim=96), _lib.TQ_ERR_INVALID_ARGUMENT, b"power-of-two"),   # Hadamard keys
+        (dict(v_rot_kind=0, v_dim=96), _lib.TQ_ERR_INVALID_ARGUMENT, b"power-of-two"),
+        (dict(mask_kind=1), _lib.TQ_ERR_INVALID_ARGUMENT, b"mask"),
+        (dict(mask_kind=7, mask=fake, mstrides=fake), _lib.TQ_ERR_INVALID_ARGUMENT, b"mask_kind"),
+        (dict(k_bits=5), _lib.TQ_ERR_INVALID_ARGUMENT, b"k_bits"),
+        (dict(kv_kind=_lib.TQ_KV_PROD, k_rot_kind=1), _lib.TQ_ERR_INVALID_ARGUMENT, b"Prod"),
+        (dict(kv_kind=_lib.TQ_KV_PROD), _lib.TQ_ERR_INVALID_ARGUMENT, b"projection"),
+        (dict(Hkv=7), _lib.TQ_ERR_INVALID_ARGUMENT, b"heads"),
+        (dict(kv_kind=_lib.TQ_KV_PLAIN, kv_dtype=0), _lib.TQ_ERR_INVALID_ARGUMENT, b"plain"),
+    ]
+    for kw, code, text in bad:
+        args = dict(ok)
+        args.update(kw)
+        assert lib.tq_attention_general(*_general_args(**args)) == code, kw
+        assert text in lib.tq_last_error(), (kw, lib.tq_last_error())
+    # the workspace query covers the tuned entry point's shapes too
+    assert lib.tq_attention_general_workspace_size(1, 32, 8, 1, 128, 64, 4096) > 0
+    assert lib.tq_attention_workspace_size(1, 32, 8, 1, 512, 4096) >= \
+        lib.tq_attention_general_workspace_size(1, 32, 8, 1, 512, 512, 4096)
 
 
 def test_check_maps_status_to_exceptions():

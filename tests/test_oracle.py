@@ -460,3 +460,94 @@ def test_prod_attention_against_sdpa_and_score_prepared(bits):
         p = np.exp(sc - sc.max(axis=-1, keepdims=True))
         o = (p @ V[b, g]) / p.sum(axis=-1, keepdims=True)
         np.testing.assert_allclose(got[b, h], o, atol=1e-9)
+
+
+def _sdpa_masked(qs, K, V, R, keep=None, add=None):
+    """torch float64 SDPA of one sequence with per-query-head masks (Hq, L, T)."""
+    Kt = torch.from_numpy(K).repeat_interleave(R, dim=0)
+    Vt = torch.from_numpy(V).repeat_interleave(R, dim=0)
+    mask = torch.from_numpy(keep) if keep is not None else torch.from_numpy(add)
+    return torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(qs), Kt, Vt, attn_mask=mask, scale=1.0).numpy()
+
+
+@pytest.mark.parametrize("form", ["bool2d", "bool4d", "add5d", "add3d"])
+@pytest.mark.parametrize("v_rot_kind", ["hadamard", "dense"])
+def test_attention_array_masks_against_sdpa(form, v_rot_kind):
+    """attention(mask=...) equals torch SDPA over the dequantized cache with the
+    mask laid out per query head by the reference's rule (_apply_attention_mask,
+    :5101-5108): the mask is broadcast against the grouped scores
+    (B, Hkv, R, L, T), a 4-D mask getting its repeat axis at position 2, so
+    query head h = g*R + r reads mask[b, g, r].  Also covers K and V of
+    different dims and rotation kinds (the output takes the value dim)."""
+    rng = np.random.default_rng(hash((form, v_rot_kind)) % 1000)
+    B, Hq, Hkv, L, T, dk = 2, 6, 2, 3, 50, 64
+    dv = 64 if v_rot_kind == "hadamard" else 48
+    R = Hq // Hkv
+    kr, kb = O.rht_signs(dk, 0), 3
+    kp, kn = O.quantize_rht(rng.standard_normal((B, Hkv, T, dk)).astype(np.float32), kb, kr,
+                            O.beta_codebook(dk, kb))
+    vr = O.rht_signs(dv, 1) if v_rot_kind == "hadamard" else O.rotation_matrix(dv, 1)
+    vx = rng.standard_normal((B, Hkv, T, dv)).astype(np.float32)
+    if v_rot_kind == "hadamard":
+        vp, vn = O.quantize_rht(vx, 2, vr, O.beta_codebook(dv, 2))
+    else:
+        vp, vn, _ = O.quantize_dense(vx, 2, vr, O.beta_codebook(dv, 2))
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, dk)).astype(np.float32), "bf16")
+    shapes = {"bool2d": (L, T), "bool4d": (B, Hkv, L, T), "add5d": (B, Hkv, R, L, T),
+              "add3d": (R, L, T)}
+    if form.startswith("bool"):
+        m = rng.random(shapes[form]) < 0.6
+        m[..., 0] = True  # no row fully masked (SDPA gives NaN there)
+    else:
+        m = rng.normal(0, 3, shapes[form]).astype(np.float32)
+    got = O.attention(q, kp, kn, vp, vn, k_bits=kb, v_bits=2, k_codebook=O.beta_codebook(dk, kb),
+                      v_codebook=O.beta_codebook(dv, 2), rot_kind="hadamard", k_rot=kr, v_rot=vr,
+                      scale=0.125, q_dtype="bf16", v_dim=dv, mask=m, v_rot_kind=v_rot_kind)
+    K = O.dequantize(kp, kn, kb, dk, O.beta_codebook(dk, kb), "hadamard", kr)
+    V = O.dequantize(vp, vn, 2, dv, O.beta_codebook(dv, 2), v_rot_kind, vr)
+    qs = O.scale_queries(q, 0.125, "bf16").astype(np.float64)
+    # per query head: explicit index arithmetic, not a broadcast
+    per_head = np.zeros((B, Hq, L, T), m.dtype)
+    for b in range(B):
+        for h in range(Hq):
+            g, r = h // R, h % R
+            if form == "bool2d":
+                per_head[b, h] = m
+            elif form == "bool4d":
+                per_head[b, h] = m[b, g]
+            elif form == "add5d":
+                per_head[b, h] = m[b, g, r]
+            else:
+                per_head[b, h] = m[r]
+    for b in range(B):
+        want = _sdpa_masked(qs[b], K[b], V[b], R,
+                            keep=per_head[b] if form.startswith("bool") else None,
+                            add=None if form.startswith("bool") else per_head[b].astype(np.float64))
+        np.testing.assert_allclose(got[b], want, atol=1e-9)
+
+
+def test_mask_broadcast_rejects_query_head_masks_on_grouped_scores():
+    """A 4-D mask broadcasts over kv heads, as the reference's expand_dims at
+    axis 2 does: a per-query-head (B, Hq, L, T) mask with Hq != Hkv does not
+    broadcast there (the fp16 layers' SDPA takes it instead)."""
+    m = np.ones((1, 8, 2, 10), bool)
+    assert O.mask_5d(m[:, :2], 1, 2, 4, 2, 10).shape == (1, 2, 4, 2, 10)
+    with pytest.raises(ValueError):
+        O.mask_5d(m, 1, 2, 4, 2, 10)
+
+
+def test_plain_attention_mask_against_sdpa():
+    rng = np.random.default_rng(77)
+    B, Hq, Hkv, L, T, d = 2, 4, 2, 3, 30, 32
+    k = O.round_to_dtype(rng.standard_normal((B, Hkv, T, d)).astype(np.float32), "f16")
+    v = O.round_to_dtype(rng.standard_normal((B, Hkv, T, 48)).astype(np.float32), "f16")
+    q = O.round_to_dtype(rng.standard_normal((B, Hq, L, d)).astype(np.float32), "f16")
+    m = rng.random((B, Hq, L, T)) < 0.7
+    m[..., 0] = True
+    got = O.attention_plain(q, k, v, scale=0.2, q_dtype="f16", mask=m)
+    qs = O.scale_queries(q, 0.2, "f16").astype(np.float64)
+    for b in range(B):
+        want = _sdpa_masked(qs[b], k[b].astype(np.float64), v[b].astype(np.float64), Hq // Hkv,
+                            keep=m[b])
+        np.testing.assert_allclose(got[b], want, atol=1e-9)

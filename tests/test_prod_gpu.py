@@ -195,9 +195,9 @@ def test_prod_left_padded_rows(device):
     _prod_case(device, 8, 2, 8, 2, 1, 2100, 128, 4, 3, starts=[0, 1500])
 
 
-def test_prod_rejects_unbuilt_shapes(device):
-    with pytest.raises(NotImplementedError):
-        _prod_case(device, 9, 1, 32, 8, 4, 300, 128, 3, 3)   # 16 rows per kv head
+def test_prod_sixteen_rows_per_kv_head(device):
+    """16 query rows per kv head run the general kernels (tq_attention_prod routes them)."""
+    _prod_case(device, 9, 1, 32, 8, 4, 300, 128, 3, 3)
 
 
 def test_cache_with_prod_keys_decode_and_save_load(device, tmp_path):
