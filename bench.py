@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE / WRITE_SIZE passes over this script scaled by the counters' reading
 # of torch's f32 -> f16 copy of known size (read x 1.9996, write x 0.9999); the
 # counter runs and the calibration are summarised with the committed profiles.
-CFG1_TRAFFIC_BYTES = 28_820_702
+CFG1_TRAFFIC_BYTES = 28_729_404
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 CFG1 = dict(B=1, Hq=32, Hkv=8, D=128, T=32768, bits=3)
 # config 2: ragged batched decode, d=256, K4/V2, dense 256x256 rotation
