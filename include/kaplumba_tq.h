@@ -71,7 +71,8 @@ int tq_packed_width(int dim, int bits);
  *   idx_i = #{ m : y_i > midpoints[m] }   (2^bits - 1 ascending midpoints)
  * and writes the packed row and the norm at token position offset + l of the
  * (b, h) row of the destination buffers (capacity tokens per (b, h)).
- * Hadamard: dim a power of two in [32, 512].  Dense: dim in {64, 128, 256}.
+ * Hadamard: dim a power of two in [32, 512].  Dense: dim a multiple of 8 in
+ * [8, 512] (64 / 128 / 256 on the matrix cores, other dims on the vector ALUs).
  * bits in 1..4.  x_dtype: F32/F16/BF16.  norm_dtype: F32 or F16.
  */
 int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,

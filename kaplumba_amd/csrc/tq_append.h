@@ -55,6 +55,25 @@ int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hip
 // widths or v_bits = k_bits + 1); returns -1 for other cases.
 int launch_append_dense_kv(const AppendArgs& k, const AppendArgs& v, int dim, int kbits, int vbits,
                            int x_dtype, hipStream_t st);
+// Dense rotation at any dim (multiples of 8 up to 512) on the vector ALUs
+// (tq_append_general.hip), for the dims the matrix-core kernels do not take.
+int launch_append_dense_general(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st);
+
+struct DequantGeneralArgs {
+  const uint32_t* packed;
+  const void* norms;
+  int norm_dtype;
+  int B, H, T, D, bits, PW;
+  int64_t cap;
+  const float* cb;
+  int rot_kind;
+  const float* rot;
+  float scale;  // f32(1/sqrt(D)), Hadamard only
+  float* out;
+};
+// Dequantize at any dim (multiples of 8 up to 512; Hadamard: powers of two).
+int launch_dequant_general(const DequantGeneralArgs& a, int64_t n_vec, hipStream_t st);
+
 // The same product for f32 input with a one-bit output (x @ R^T >= 0), the
 // Prod codec's QJL signs; norms receive ||x||.
 int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st);

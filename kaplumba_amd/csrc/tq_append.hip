@@ -491,8 +491,10 @@ extern "C" int tq_dequantize(const uint32_t* packed, const void* norms, int norm
                              const float* codebook, int rot_kind, const float* rot, float* out,
                              void* stream) {
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: bits %d", bits);
-  if (dim < 32 || dim > 256 || (dim & (dim - 1)))
-    return fail(TQ_ERR_UNSUPPORTED, "dequantize: dim %d (pow2 32..256)", dim);
+  if (dim < 8 || dim > 512 || dim % 8)
+    return fail(TQ_ERR_UNSUPPORTED, "dequantize: dim %d (multiples of 8 up to 512)", dim);
+  if (rot_kind == TQ_ROT_HADAMARD && (dim & (dim - 1)))
+    return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: Hadamard rotation needs a power-of-two dim, got %d", dim);
   if (T < 0 || T > capacity) return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: T > capacity");
   if (rot_kind != TQ_ROT_HADAMARD && rot_kind != TQ_ROT_DENSE)
     return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: rot_kind %d", rot_kind);
@@ -500,6 +502,12 @@ extern "C" int tq_dequantize(const uint32_t* packed, const void* norms, int norm
   if (n == 0) return TQ_OK;
   if (!packed || !norms || !codebook || !rot || !out)
     return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: null pointer");
+  if (dim < 32 || dim > 256 || (dim & (dim - 1))) {
+    const DequantGeneralArgs g{packed, norms, norm_dtype, B, H, T, dim, bits,
+                               tq_packed_width(dim, bits), capacity, codebook, rot_kind, rot,
+                               static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim))), out};
+    return launch_dequant_general(g, n, static_cast<hipStream_t>(stream));
+  }
   DequantArgs a{packed, norms, norm_dtype, B, H, T, dim, bits, tq_packed_width(dim, bits),
                 capacity, codebook, rot_kind, rot,
                 static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim))), out};

@@ -406,7 +406,7 @@ int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hip
     case 128: return launch_dense_dim<128>(a, bits, x_dtype, st);
     case 256: return launch_dense_dim<256>(a, bits, x_dtype, st);
   }
-  return fail(TQ_ERR_UNSUPPORTED, "append: dense rotation needs dim in {64, 128, 256}, got %d", dim);
+  return launch_append_dense_general(a, dim, bits, x_dtype, st);
 }
 
 }  // namespace tq

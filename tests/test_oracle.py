@@ -551,3 +551,19 @@ def test_plain_attention_mask_against_sdpa():
         want = _sdpa_masked(qs[b], k[b].astype(np.float64), v[b].astype(np.float64), Hq // Hkv,
                             keep=m[b])
         np.testing.assert_allclose(got[b], want, atol=1e-9)
+
+
+@pytest.mark.parametrize("d", [8, 24, 40, 96, 160, 320, 480])
+def test_norm_tree_at_any_dim(d):
+    """norm_f32 at a dim that is not a power of two: the zero padding leaves the
+    value that of the padded power-of-two vector, within an ulp of the float64
+    norm, and the tree of a dim below 32 equals the in-lane fold of one padded
+    32-element lane."""
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal((50, d)).astype(np.float32) * np.float32(3.0)
+    got = O.norm_f32(x)
+    exact = np.sqrt((x.astype(np.float64) ** 2).sum(axis=-1))
+    assert np.all(np.abs(got - exact) <= 2 * np.spacing(exact.astype(np.float32)))
+    lanes = 32 << max(0, (-(-d // 32) - 1).bit_length()) if d > 32 else 32
+    padded = np.concatenate([x, np.zeros((50, lanes - d), np.float32)], axis=-1)
+    assert np.array_equal(got, O.norm_f32(padded))
