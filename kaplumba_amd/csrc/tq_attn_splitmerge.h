@@ -194,6 +194,10 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_rot_kernel(const flo
   const float* pml_g = pml + grp * static_cast<int64_t>(n_splits) * NQ * 2;
   const int c = tid % C4;
   const int sg = tid / C4;
+  // R_V^-1's signs, loaded with the partials (not after the fold: one round trip)
+  float vr[QE];
+#pragma unroll
+  for (int e = 0; e < QE; ++e) vr[e] = tid < kWave ? vrot[tid + e * kWave] : 0.f;
   float M = -INFINITY, Lsum = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int sp0 = sg; sp0 < nvalid; sp0 += SG * BATCH) {
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_rot_kernel(const flo
     const int64_t qo = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + j / p.L) * p.L + j % p.L) * D;
 #pragma unroll
     for (int e = 0; e < QE; ++e)
-      store_out(p.out, p.q_dtype, qo + tid + e * kWave, y[e] * p.rscale * vrot[tid + e * kWave]);
+      store_out(p.out, p.q_dtype, qo + tid + e * kWave, y[e] * p.rscale * vr[e]);
   }
 }
 

@@ -523,17 +523,28 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     stage(slot, sub_start(i + NS));
     slot = slot + 1 == NS ? 0 : slot + 1;
 
-    // ---- scores: D / 8 MFMAs in two alternating accumulator chains
+    // ---- scores: D / 8 MFMAs in two alternating accumulator chains; the
+    // table reads run KPF MFMAs ahead (about a dozen reads in flight, within
+    // the lgkm counter), which hides the LDS latency behind the products
     f32x4_t Ch = {0.f, 0.f, 0.f, 0.f}, Cl = {0.f, 0.f, 0.f, 0.f};
+    {
+      constexpr int KPF = 6;
+      uint2 eb[D / 8][2];
+      auto kload = [&](int j) {
+        eb[j][0] = lds_at<uint2>(lds, S::LUTK_OFF + key_addr<2 * KB, S::LOGSK>(kw, (4 * j) * KB, lutk_lane, kmask));
+        eb[j][1] = lds_at<uint2>(lds, S::LUTK_OFF + key_addr<2 * KB, S::LOGSK>(kw, (4 * j + 2) * KB, lutk_lane, kmask));
+      };
 #pragma unroll
-    for (int j = 0; j < D / 8; ++j) {
-      const uint2 e0 = lds_at<uint2>(lds, S::LUTK_OFF + key_addr<2 * KB, S::LOGSK>(kw, (4 * j) * KB, lutk_lane, kmask));
-      const uint2 e1 = lds_at<uint2>(lds, S::LUTK_OFF + key_addr<2 * KB, S::LOGSK>(kw, (4 * j + 2) * KB, lutk_lane, kmask));
-      const u32x4_t a = {e0.x, e0.y, e1.x, e1.y};
-      if (j & 1)
-        Cl = mfma_f16(a, qd[j], Cl);
-      else
-        Ch = mfma_f16(a, qd[j], Ch);
+      for (int j = 0; j < KPF && j < D / 8; ++j) kload(j);
+#pragma unroll
+      for (int j = 0; j < D / 8; ++j) {
+        if (j + KPF < D / 8) kload(j + KPF);
+        const u32x4_t a = {eb[j][0].x, eb[j][0].y, eb[j][1].x, eb[j][1].y};
+        if (j & 1)
+          Cl = mfma_f16(a, qd[j], Cl);
+        else
+          Ch = mfma_f16(a, qd[j], Ch);
+      }
     }
     const f32x4_t C = Ch + Cl;
 
@@ -630,16 +641,25 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     const uint32_t x23 = row_ror_u<12>(w23);
     const u32x4_t A0 = {w01, w01, w23, w23};
     const u32x4_t A1 = {x01, x01, x23, x23};
+    // value table reads run VPF coordinates (two MFMAs each) ahead
+    {
+      constexpr int VPF = 4;
+      uint2 vop[CPL][4];
+      auto vload = [&](int c) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      uint2 vop[4];
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const uint32_t z[1] = {(c & 1) ? zh[e2] : zl[e2]};
+          vop[c][e2] = lds_at<uint2>(lds, S::LUTV_OFF + key_addr<2 * VB, S::LOGSV>(z, (c >> 1) * 2 * VB, lutv_lane, vmask));
+        }
+      };
 #pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const uint32_t z[1] = {(c & 1) ? zh[e2] : zl[e2]};
-        vop[e2] = lds_at<uint2>(lds, S::LUTV_OFF + key_addr<2 * VB, S::LOGSV>(z, (c >> 1) * 2 * VB, lutv_lane, vmask));
+      for (int c = 0; c < VPF && c < CPL; ++c) vload(c);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        if (c + VPF < CPL) vload(c + VPF);
+        O[c] = mfma_f16(A0, u32x4_t{vop[c][0].x, vop[c][0].y, vop[c][1].x, vop[c][1].y}, O[c]);
+        O[c] = mfma_f16(A1, u32x4_t{vop[c][2].x, vop[c][2].y, vop[c][3].x, vop[c][3].y}, O[c]);
       }
-      O[c] = mfma_f16(A0, u32x4_t{vop[0].x, vop[0].y, vop[1].x, vop[1].y}, O[c]);
-      O[c] = mfma_f16(A1, u32x4_t{vop[2].x, vop[2].y, vop[3].x, vop[3].y}, O[c]);
     }
   }
   // the trailing transfers (past t_end: zeros) land before the workgroup ends
