@@ -226,7 +226,8 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   // d <= 128 and 4 rows per kv head, or 1-bit Prod) run the general kernels.
   const bool tuned_dim = dim == 64 || dim == 128 || dim == 256;
   const bool prod_small = prod && dim <= 128 && static_cast<int64_t>(Hq / Hkv) * L <= 4 && k_bits >= 1;
-  if (!tuned_dim || (prod && !prod_small)) {
+  const bool tile = !prod && tile_rows_path(kv_kind, dim, dim, (Hq / Hkv) * L);
+  if (!tuned_dim || (prod && !prod_small) || tile) {
     GenCall c{};
     c.q = q;
     c.q_dtype = q_dtype;

@@ -91,8 +91,16 @@ struct GenParams {
   float* pml;    // [B*Hkv*n_rg, n_splits, 8, 2]
   float rscale_k, rscale_v;  // f32(1/sqrt(Dk)), f32(1/sqrt(Dv))
   float qjl_scale;           // f32(sqrt(pi/2) / Dk)
+  int po_natural;            // partials already through R_V^-1 (the tile kernel, Hadamard values)
+  uint32_t* qhl;             // tile kernel: per query row, q_rot * sq as hi then lo f16 [rows, 2, Dk / 2] u32
+  float* qsq;                // tile kernel: sq per query row
   void* out;                 // [B, Hq, L, Dv] in the query dtype
 };
+
+// Query rows per kv head from which packed caches at d = 128 run the tile
+// kernel (tq_attn_tile.h): its K/V decode is shared by 128 rows.
+constexpr int kTileMinRows = 64;
+bool tile_rows_path(int kv_kind, int Dk, int Dv, int rows);
 
 // Workspace bytes of the general path for this problem.
 int64_t general_workspace_bytes(int B, int Hq, int Hkv, int L, int Dk, int Dv, int64_t T,

@@ -1,8 +1,11 @@
 // Kernels and host side of the general attention path (see tq_attn_general.h).
 #include <algorithm>
 
+#include <cstdlib>
+
 #include "tq_attn_general.h"
 #include "tq_attn_merge.h"
+#include "tq_attn_tile.h"
 
 namespace tq {
 namespace {
@@ -45,24 +48,36 @@ __global__ __launch_bounds__(kGenThreads) void gen_qprep_kernel(GenParams p, int
                                                                 float* __restrict__ dst) {
   __shared__ float4 s_q4[kQpRows * kGenMaxDim / 4];
   __shared__ float s_part[4][kQpRows][64];
+  __shared__ int64_t s_off[kQpRows];
   float* s_q = reinterpret_cast<float*>(s_q4);
   const int tid = threadIdx.x;
   const int Dk = p.Dk;
   const int DkP = p.DkP;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kQpRows;
-  for (int idx = tid; idx < kQpRows * DkP; idx += kGenThreads) {
-    const int r = idx / DkP;
-    const int d = idx % DkP;
-    const int64_t row = row0 + r;
-    float v = 0.f;
-    if (row < n_rows && d < Dk) {
-      const int l = static_cast<int>(row % p.L);
-      const int64_t bh = row / p.L;
-      const int h = static_cast<int>(bh % p.Hq);
-      const int64_t b = bh / p.Hq;
-      v = round_to<QDT>(load_elem<QDT>(p.q, b * p.q_sb + h * p.q_sh + l * p.q_sl + d) * p.scale_q);
+  const int nr = static_cast<int>(n_rows - row0 < kQpRows ? n_rows - row0 : kQpRows);  // rows of this block
+  // element offset of each row's query (one division chain per row; rows
+  // past the end repeat the block's first row and are dropped below)
+  if (tid < kQpRows) {
+    const int64_t row = row0 + (tid < nr ? tid : 0);
+    const int l = static_cast<int>(row % p.L);
+    const int64_t bh = row / p.L;
+    const int h = static_cast<int>(bh % p.Hq);
+    const int64_t b = bh / p.Hq;
+    s_off[tid] = b * p.q_sb + h * p.q_sh + l * p.q_sl;
+  }
+  __syncthreads();
+  // all of a thread's loads are issued before the first is used
+  for (int d0 = 0; d0 < DkP; d0 += kGenThreads) {
+    const int d = d0 + tid;
+    const int dc = d < Dk ? d : 0;
+    float v[kQpRows];
+#pragma unroll
+    for (int r = 0; r < kQpRows; ++r) v[r] = load_elem<QDT>(p.q, s_off[r] + dc);
+    if (d < DkP) {
+#pragma unroll
+      for (int r = 0; r < kQpRows; ++r)
+        s_q[r * DkP + d] = (r < nr && d < Dk) ? round_to<QDT>(v[r] * p.scale_q) : 0.f;
     }
-    s_q[idx] = v;
   }
   __syncthreads();
   if (mode == 2) {
@@ -105,30 +120,30 @@ __global__ __launch_bounds__(kGenThreads) void gen_qprep_kernel(GenParams p, int
   }
   float scl = 1.f;
   if (mode == 1) {
-    for (int idx = tid; idx < kQpRows * DkP; idx += kGenThreads) {
-      const int d = idx % DkP;
-      if (d < Dk) s_q[idx] *= mat[d];
-    }
+    for (int r = 0; r < kQpRows; ++r)
+      for (int d = tid; d < Dk; d += kGenThreads) s_q[r * DkP + d] *= mat[d];
     __syncthreads();
-    // butterflies of distance 1, 2, ..., Dk/2 over each row (stride DkP)
+    // butterflies of distance 1, 2, ..., Dk/2 over each row (stride DkP):
+    // thread (row r0 + j * rpp, pair k); Dk is a power of two here
+    const int hp = Dk / 2;
+    const int rpp = hp < kGenThreads ? kGenThreads / hp : 1;
+    const int r0 = tid / hp;
+    const int k0 = tid % hp;
     for (int hs = 1; hs < Dk; hs <<= 1) {
-      for (int idx = tid; idx < kQpRows * (Dk / 2); idx += kGenThreads) {
-        const int r = idx / (Dk / 2);
-        const int k = idx % (Dk / 2);
-        const int i0 = r * DkP + (k / hs) * 2 * hs + (k % hs);
-        const float a = s_q[i0];
-        const float b = s_q[i0 + hs];
-        s_q[i0] = a + b;
-        s_q[i0 + hs] = a - b;
-      }
+      for (int k = k0; k < hp; k += kGenThreads)
+        for (int r = r0; r < kQpRows; r += rpp) {
+          const int i0 = r * DkP + ((k & ~(hs - 1)) << 1) + (k & (hs - 1));
+          const float a = s_q[i0];
+          const float b = s_q[i0 + hs];
+          s_q[i0] = a + b;
+          s_q[i0 + hs] = a - b;
+        }
       __syncthreads();
     }
     scl = p.rscale_k;
   }
-  for (int idx = tid; idx < kQpRows * DkP; idx += kGenThreads) {
-    const int64_t row = row0 + idx / DkP;
-    if (row < n_rows) dst[row * DkP + idx % DkP] = s_q[idx] * scl;
-  }
+  for (int r = 0; r < nr; ++r)
+    for (int d = tid; d < DkP; d += kGenThreads) dst[(row0 + r) * DkP + d] = s_q[r * DkP + d] * scl;
 }
 
 // -------------------------------------------------------------- partial ---
@@ -509,7 +524,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_merge_kernel(GenParams p) {
     s_y[idx] = y;
   }
   __syncthreads();
-  const bool plain = p.key_kind == kGenPlainF16 || p.key_kind == kGenPlainBf16;
+  const bool plain = p.key_kind == kGenPlainF16 || p.key_kind == kGenPlainBf16 || p.po_natural;
   auto out_off = [&](int i) {
     const int rr = row0 + i;
     return ((static_cast<int64_t>(b) * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L) * Dv;
@@ -566,6 +581,66 @@ __global__ __launch_bounds__(kGenThreads) void gen_merge_kernel(GenParams p) {
   }
 }
 
+// Partials already in the natural basis (plain values, or the tile kernel's
+// Hadamard values): the merge is element-wise.  Thread = (row, 4 output
+// columns): the splits' (m, l) and o by log-sum-exp, loads in batches of 4
+// splits in flight, / max(l, 1e-6), output in the query dtype.
+__global__ __launch_bounds__(256) void gen_merge_flat_kernel(GenParams p, int64_t n_items) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n_items) return;
+  const int C4 = p.Dv / 4;
+  const int RL = p.R * p.L;
+  const int c4 = static_cast<int>(idx % C4);
+  const int64_t row = idx / C4;  // (b * Hkv + gk) * RL + rr
+  const int rr = static_cast<int>(row % RL);
+  const int64_t bg = row / RL;
+  const int gk = static_cast<int>(bg % p.Hkv);
+  const int64_t b = bg / p.Hkv;
+  const int64_t gi = bg * p.n_rg + rr / 8;
+  const int ri = rr % 8;
+  const int ns = p.n_splits;
+  float M = -INFINITY, Lsum = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k0 = 0; k0 < ns; k0 += 4) {
+    float2 ml[4];
+    float4 oo[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = k0 + u;
+      const int64_t r = (gi * ns + k) * kGenNQ + ri;
+      ml[u] = k < ns ? reinterpret_cast<const float2*>(p.pml)[r] : make_float2(-INFINITY, 0.f);
+      oo[u] = (k < ns && ml[u].x != -INFINITY) ? reinterpret_cast<const float4*>(p.po + r * p.Dv)[c4]
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float bm = M;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bm = fmaxf(bm, ml[u].x);
+    if (bm == -INFINITY) continue;
+    const float r0 = M == -INFINITY ? 0.f : expf(M - bm);
+    Lsum *= r0;
+    acc.x *= r0;
+    acc.y *= r0;
+    acc.z *= r0;
+    acc.w *= r0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float sc = ml[u].x == -INFINITY ? 0.f : expf(ml[u].x - bm);
+      Lsum = fmaf(sc, ml[u].y, Lsum);
+      acc.x = fmaf(sc, oo[u].x, acc.x);
+      acc.y = fmaf(sc, oo[u].y, acc.y);
+      acc.z = fmaf(sc, oo[u].z, acc.z);
+      acc.w = fmaf(sc, oo[u].w, acc.w);
+    }
+    M = bm;
+  }
+  const float inv = M == -INFINITY ? 0.f : 1.f / fmaxf(Lsum, kNormEps);
+  const int64_t o = ((b * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L) * p.Dv + 4 * c4;
+  store_out(p.out, p.q_dtype, o, acc.x * inv);
+  store_out(p.out, p.q_dtype, o + 1, acc.y * inv);
+  store_out(p.out, p.q_dtype, o + 2, acc.z * inv);
+  store_out(p.out, p.q_dtype, o + 3, acc.w * inv);
+}
+
 // --------------------------------------------------------------- launch ---
 struct GenPlan {
   int n_splits, chunk, n_rg;
@@ -591,12 +666,62 @@ GenPlan gen_plan(int B, int Hq, int Hkv, int L, int64_t T) {
   return gp;
 }
 
+// The tile kernel's plan: 128-row blocks, splits aiming at one workgroup per
+// CU (its LDS holds one), whole 32-token sub-chunks.
+GenPlan tile_plan(int B, int Hq, int Hkv, int L, int64_t T) {
+  GenPlan gp{};
+  const int64_t rows = static_cast<int64_t>(Hq / Hkv) * L;
+  gp.n_rg = static_cast<int>((rows + kGenNQ - 1) / kGenNQ);
+  const int64_t blocks = static_cast<int64_t>(B) * Hkv * ((rows + kTileRows - 1) / kTileRows);
+  const int64_t target = static_cast<int64_t>(device_cu_count());
+  int64_t ns = blocks > 0 ? (target + blocks - 1) / blocks : 1;
+  ns = std::max<int64_t>(1, std::min<int64_t>(ns, (T + 255) / 256));
+  int64_t chunk = (T + ns - 1) / ns;
+  chunk = std::max<int64_t>(32, (chunk + 31) / 32 * 32);
+  if ((T + chunk - 1) / chunk > kGenMaxSplits) chunk = ((T + kGenMaxSplits - 1) / kGenMaxSplits + 31) / 32 * 32;
+  chunk = std::min<int64_t>(chunk, int64_t(1) << 30);
+  gp.chunk = static_cast<int>(chunk);
+  gp.n_splits = static_cast<int>(std::max<int64_t>(1, (T + chunk - 1) / chunk));
+  return gp;
+}
+
 int64_t a256(int64_t x) { return (x + 255) / 256 * 256; }
 int round32(int d) { return (d + 31) / 32 * 32; }
 int pow2_at_least(int d) {
   int r = 32;
   while (r < d) r <<= 1;
   return r;
+}
+
+template <int KB, int VB>
+int launch_tile(const GenParams& p, hipStream_t st) {
+  const int n_blocks = (p.R * p.L + kTileRows - 1) / kTileRows;
+  const int64_t wgs = static_cast<int64_t>(p.B) * p.Hkv * n_blocks * p.n_splits;
+  if (wgs > INT32_MAX) return fail(TQ_ERR_UNSUPPORTED, "attention: %lld tile workgroups", static_cast<long long>(wgs));
+  hipLaunchKernelGGL((gen_tile_kernel<KB, VB>), dim3(static_cast<unsigned>(wgs)), dim3(kTileThreads), 0, st, p,
+                     n_blocks);
+  return check_launch("gen_tile_kernel");
+}
+
+template <int KB>
+int launch_tile_vb(const GenParams& p, int vb, hipStream_t st) {
+  switch (vb) {
+    case 1: return launch_tile<KB, 1>(p, st);
+    case 2: return launch_tile<KB, 2>(p, st);
+    case 3: return launch_tile<KB, 3>(p, st);
+    case 4: return launch_tile<KB, 4>(p, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
+}
+
+int launch_tile_partial(const GenParams& p, int kb, int vb, hipStream_t st) {
+  switch (kb) {
+    case 1: return launch_tile_vb<1>(p, vb, st);
+    case 2: return launch_tile_vb<2>(p, vb, st);
+    case 3: return launch_tile_vb<3>(p, vb, st);
+    case 4: return launch_tile_vb<4>(p, vb, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "attention: k_bits %d not in 1..4", kb);
 }
 
 template <int KIND, int KB, int VB>
@@ -656,15 +781,30 @@ bool pow2(int d) { return d > 0 && (d & (d - 1)) == 0; }
 
 }  // namespace
 
+bool tile_rows_path(int kv_kind, int Dk, int Dv, int rows) {
+  // KAPLUMBA_TQ_TILE=0 keeps these shapes on the other kernels (comparisons)
+  static const bool enabled = [] {
+    const char* e = getenv("KAPLUMBA_TQ_TILE");
+    return !(e && e[0] == '0');
+  }();
+  return enabled && kv_kind == TQ_KV_PACKED && Dk == 128 && Dv == 128 && rows >= kTileMinRows;
+}
+
 int64_t general_workspace_bytes(int B, int Hq, int Hkv, int L, int Dk, int Dv, int64_t T, bool prod) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || Dk <= 0 || Dv <= 0 || Hq % Hkv) return 0;
   T = std::max<int64_t>(T, 1);
-  const GenPlan gp = gen_plan(B, Hq, Hkv, L, T);
+  GenPlan gp = gen_plan(B, Hq, Hkv, L, T);
   const int64_t rows = static_cast<int64_t>(B) * Hq * L;
+  int64_t tile_q = 0;  // the tile kernel's prepared query rows
+  if (tile_rows_path(TQ_KV_PACKED, Dk, Dv, (Hq / Hkv) * L)) {
+    const GenPlan tp = tile_plan(B, Hq, Hkv, L, T);
+    if (tp.n_splits > gp.n_splits) gp = tp;
+    tile_q = a256(rows * Dk * 4) + a256(rows * 4);
+  }
   const int64_t groups = static_cast<int64_t>(B) * Hkv * gp.n_rg;
   return a256(rows * round32(Dk) * 4) * (prod ? 2 : 1) +
          a256(groups * gp.n_splits * kGenNQ * static_cast<int64_t>(Dv) * 4) +
-         a256(groups * gp.n_splits * kGenNQ * 2 * 4);
+         a256(groups * gp.n_splits * kGenNQ * 2 * 4) + tile_q;
 }
 
 int general_attention(const GenCall& c) {
@@ -723,7 +863,10 @@ int general_attention(const GenCall& c) {
   if (c.max_tokens > 0 && (!c.v || (!c.k && !(prod && kb == 0))))
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null cache pointer");
   const int64_t T = std::max<int64_t>(c.max_tokens, 1);
-  const GenPlan gp = gen_plan(c.B, c.Hq, c.Hkv, c.L, T);
+  const bool tile = c.kv_kind == TQ_KV_PACKED && c.mask_kind == TQ_MASK_NONE &&
+                    tile_rows_path(c.kv_kind, c.Dk, c.Dv, (c.Hq / c.Hkv) * c.L) &&
+                    static_cast<int64_t>(c.B) * c.Hq * c.L < (int64_t(1) << 30);
+  const GenPlan gp = tile ? tile_plan(c.B, c.Hq, c.Hkv, c.L, T) : gen_plan(c.B, c.Hq, c.Hkv, c.L, T);
   if (static_cast<int64_t>(c.Hkv) * gp.n_rg > 65535 || c.B > 65535)
     return fail(TQ_ERR_UNSUPPORTED, "attention: %lld kv head row groups / %d sequences exceed one launch",
                 (long long)c.Hkv * gp.n_rg, c.B);
@@ -796,14 +939,26 @@ int general_attention(const GenCall& c) {
   p.po = reinterpret_cast<float*>(ws);
   ws += a256(groups * gp.n_splits * kGenNQ * static_cast<int64_t>(c.Dv) * 4);
   p.pml = reinterpret_cast<float*>(ws);
+  ws += a256(groups * gp.n_splits * kGenNQ * 2 * 4);
+  if (tile) {
+    p.qhl = reinterpret_cast<uint32_t*>(ws);
+    ws += a256(rows * c.Dk * 4);
+    p.qsq = reinterpret_cast<float*>(ws);
+  }
   p.rscale_k = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(c.Dk)));
   p.rscale_v = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(c.Dv)));
   p.qjl_scale = static_cast<float>(__builtin_sqrt(3.14159265358979323846 / 2.0) / c.Dk);
   p.out = c.out;
 
   hipStream_t st = static_cast<hipStream_t>(c.stream);
+  // the tile kernel takes its query rows split per row (gen_tile_qprep_kernel,
+  // which rotates Hadamard queries itself) and hands over natural-basis
+  // partials for Hadamard values
+  p.po_natural = (tile && c.v_rot_kind == TQ_ROT_HADAMARD) ? 1 : 0;
   if (plain)
     launch_qprep_mode(p, rows, 0, nullptr, p.qrot, st);
+  else if (tile && c.k_rot_kind == TQ_ROT_HADAMARD)
+    ;
   else if (c.k_rot_kind == TQ_ROT_HADAMARD && kb > 0)
     launch_qprep_mode(p, rows, 1, c.k_rot, p.qrot, st);
   else if (c.k_rot_kind == TQ_ROT_DENSE)
@@ -811,8 +966,21 @@ int general_attention(const GenCall& c) {
   if (prod) launch_qprep_mode(p, rows, 2, c.projection, p.qproj, st);
   int rc = check_launch("gen_qprep_kernel");
   if (rc) return rc;
-  rc = launch_gen_partial(p, kb, plain ? 0 : c.v_bits, st);
+  if (tile) {
+    const int64_t wgs = (rows + 63) / 64;
+    hipLaunchKernelGGL(gen_tile_qprep_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kTileQpThreads), 0, st, p,
+                       static_cast<int>(rows));
+    rc = check_launch("gen_tile_qprep_kernel");
+    if (rc) return rc;
+  }
+  rc = tile ? launch_tile_partial(p, kb, c.v_bits, st) : launch_gen_partial(p, kb, plain ? 0 : c.v_bits, st);
   if (rc) return rc;
+  if (plain || p.po_natural) {
+    const int64_t items = static_cast<int64_t>(c.B) * c.Hkv * (c.Hq / c.Hkv) * c.L * (c.Dv / 4);
+    hipLaunchKernelGGL(gen_merge_flat_kernel, dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), 0, st,
+                       p, items);
+    return check_launch("gen_merge_flat_kernel");
+  }
   const unsigned zc = (!plain && c.v_rot_kind == TQ_ROT_DENSE) ? static_cast<unsigned>((c.Dv + 63) / 64) : 1u;
   const dim3 mgrid(static_cast<unsigned>(c.Hkv * gp.n_rg), static_cast<unsigned>(c.B), zc);
   hipLaunchKernelGGL(gen_merge_kernel, mgrid, dim3(kGenThreads), 0, st, p);

@@ -29,10 +29,10 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
 
 // Round-to-nearest-even f32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // NaN stays a (quiet) NaN; a select, so unrolled callers stay straight-line
+  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : rne);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {

@@ -352,3 +352,22 @@ def test_plain_layers(device, kvdt, d, Hq, Hkv, L, T, lengths):
     out = ops.attention_plain(q_tensor(q, "bf16", device), kb[:, :, :T], vb[:, :, :T],
                               1 / math.sqrt(d), causal, seq_lens=sl)
     assert_close(out, want, "bf16", f"plain {kvdt} d{d} Hq{Hq} Hkv{Hkv} L{L} T{T}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,kb,vb,rot,lengths,starts,qdt,norm", [
+    (8, 1, 9, 3, 3, "hadamard", None, None, "bf16", "float32"),          # 72 rows: one partial block
+    (32, 8, 25, 4, 2, "hadamard", [3000, 17], None, "bf16", "float32"),  # 100 rows, ragged (one short)
+    (16, 4, 50, 2, 1, "dense", None, None, "f16", "float16"),            # 200 rows: full + partial block
+    (4, 1, 64, 1, 4, "hadamard", [1500, 1500], [0, 700], "bf16", "float32"),  # left padding
+    (8, 2, 32, 4, 4, "hadamard", [33, 2000], None, "f32", "float32"),    # 128 rows, a 33-token sequence
+    (2, 1, 80, 3, 3, "hadamard", None, None, "bf16", "float16"),         # L > T - causal rows see nothing
+])
+def test_tile_rows(device, Hq, Hkv, L, kb, vb, rot, lengths, starts, qdt, norm):
+    """64 or more query rows per kv head at d = 128: the tile kernel (K/V decoded
+    into LDS once per 32-token sub-chunk and shared by 128 rows)."""
+    B = 1 if lengths is None else len(lengths)
+    T = 1100 if lengths is None else max(lengths)
+    if L == 80:
+        T = 60  # more queries than keys: the first rows see no key (uniform weights)
+    run_case(device, 900 + L + kb, B, Hq, Hkv, L, T, 128, kb, vb, rot=rot, qdt=qdt, norm=norm,
+             lengths=lengths, starts=starts)
