@@ -16,13 +16,14 @@
 //           products.  The two 16-token tiles hold tokens 8 (m / 4) + 4 h +
 //           m % 4 in row m of tile h, so lane (row n, g) ends with tokens
 //           8 g .. 8 g + 7;
-//   decode  sub-chunk i + 1 (while the score products run): thread (token,
-//           8 coordinates) looks up the K and V pair tables and writes 16
-//           bytes each of the hi and lo f16 parts of the scaled codebook
-//           values; K rows go to the slot the score MFMA reads them from, V
-//           rows into 16-column blocks (32 bytes per token, token slots
-//           permuted so a transposed read meets every bank once), one
-//           block per wave so the stores also spread over all banks;
+//   decode  sub-chunk i + 1, by the four lead waves after their score
+//           products: thread (token, 8 coordinates) looks up the K and V
+//           pair tables and writes 16 bytes each of the hi and lo f16 parts
+//           of the scaled codebook values; K rows go to the slot the score
+//           MFMA reads them from, V rows into 16-column blocks (32 bytes per
+//           token, token slots permuted so a transposed read meets every
+//           bank once), whole blocks per wave so the stores also spread over
+//           all banks;
 //   softmax in log2 units with a lazy reference maximum (moved only when a
 //           score exceeds it by 2^7) and a lazy value-norm exponent, checked
 //           by one vote per sub-chunk;
@@ -86,9 +87,7 @@ struct TileShape {
   // staging loads: one thread per word / norm, in staging order
   static constexpr int LOAD_SLOTS = SUB * PWK + SUB * PWV + 2 * SUB;
   static constexpr int LOADS = (LOAD_SLOTS + kTileThreads - 1) / kTileThreads;
-  // decode units (token, 8 coordinates) per thread
-  static constexpr int DU = SUB * (D / 8) / kTileThreads;
-  static_assert(DU * kTileThreads == SUB * (D / 8) && kTileThreads >= 2 * SUB, "decode split");
+  static_assert(kTileThreads >= 4 * SUB, "norm copy by the lead waves");
   static_assert(BYTES <= 160 * 1024, "tile kernel LDS");
   static_assert(KROW % 16 == 0 && STG_BYTES % 16 == 0 && DEC_BYTES % 16 == 0, "16-byte aligned LDS rows");
   static_assert(STG_V == SUB * PWK * 4 && STG_KN == STG_V + SUB * PWV * 4, "staging in load-slot order");
@@ -325,42 +324,54 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
     *reinterpret_cast<uint2*>(lds + S::VTAB_OFF + e * 8) = make_uint2(h0 | (h1 << 16), l0 | (l1 << 16));
   }
 
-  // ---- decode of one sub-chunk: every thread does 8 coordinates of a key
-  // row and 8 of a value row.  Keys: thread (token tid / 16, c8 = tid % 16),
-  // 16 lanes filling one 256-byte row.  Values: wave w fills the 16-column
-  // block w (one KiB: lane (token lane / 2, half lane % 2)), so a wave's
-  // stores cover every bank evenly.  All offsets are fixed per thread.
-  static_assert(kTileNW == D / 16 && SUB == 32 && S::DU == 1, "decode mapping: 8 waves x 16-column blocks");
+  // ---- decode of one sub-chunk, by the four lead waves (which otherwise
+  // wait at the step's barrier for the trailing ones): every lead thread does
+  // 8 coordinates of two key rows and of two value rows.  Keys: thread
+  // (token tid / 16 + 16 u, c8 = tid % 16), 16 lanes filling one 256-byte
+  // row.  Values: wave w fills the 16-column blocks w and w + 4 (one KiB
+  // each: lane (token lane / 2, half lane % 2)), so a wave's stores cover
+  // every bank evenly.  All offsets are fixed per thread.
+  static_assert(kTileNW == D / 16 && SUB == 32, "decode mapping: 4 lead waves x two 16-column blocks");
   const uint32_t ktab_lane = S::KTAB_OFF + (lane % S::REPK) * 8;
   const uint32_t vtab_lane = S::VTAB_OFF + (lane % S::REPV) * 8;
-  const int kdt = tid >> 4, kc8 = tid & 15;
-  const int vdt = lane >> 1, vc8 = 2 * wave + (lane & 1);
-  const uint32_t dk_off = tile_kslot(kdt) * S::KROW + kc8 * 16;
-  const uint32_t dv_off = wave * S::VCT + tile_vslot(vdt) * 32 + (lane & 1) * 16;
-  // staging word holding the first bit of the 8 coordinates, and the shift
+  const int kdt = (tid >> 4) & 15, kc8 = tid & 15;
+  const int vdt = lane >> 1;
+  const int vc8 = 2 * (wave & 3) + (lane & 1);  // 16-column blocks wave % 4 and wave % 4 + 4
   const uint32_t ks_off = S::STG_K + (kdt * S::PWK + ((8 * KB * kc8) >> 5)) * 4;
+  const uint32_t dk_off = tile_kslot(kdt) * S::KROW + kc8 * 16;
   const uint32_t vs_off = S::STG_V + (vdt * S::PWV + ((8 * VB * vc8) >> 5)) * 4;
+  const uint32_t dv_off = (vc8 >> 1) * S::VCT + tile_vslot(vdt) * 32 + (lane & 1) * 16;
   const int ksh = (8 * KB * kc8) & 31;
   const int vsh = (8 * VB * vc8) & 31;
+  // the second unit (tokens + 16, blocks + 4) sits at fixed distances:
+  // tile_kslot(t + 16) = tile_kslot(t) + 8, coordinates + 64 start 8 VB
+  // bytes further in a value row with the same shift
+  constexpr uint32_t kStepK = 16 * S::PWK * 4, kStepDK = 8 * S::KROW;
+  constexpr uint32_t kStepV = 8 * VB, kStepDV = 4 * S::VCT;
   auto decode = [&](int sb, int db) {
     const unsigned char* st = lds + S::STG_OFF + sb * S::STG_BYTES;
     unsigned char* dc = lds + S::DEC_OFF + db * S::DEC_BYTES;
-    // the word after a row's last one is still staging memory; its bits
-    // land above the 8 * BITS used ones
-    const uint32_t* wk = reinterpret_cast<const uint32_t*>(st + ks_off);
-    const uint32_t* wv = reinterpret_cast<const uint32_t*>(st + vs_off);
-    const uint32_t xk = __builtin_amdgcn_alignbit(wk[1], wk[0], ksh);
-    const uint32_t xv = __builtin_amdgcn_alignbit(wv[1], wv[0], vsh);
-    uint2 ek[4], ev[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      ek[m] = lds_at<uint2>(lds, ktab_lane + ((xk >> (2 * m * KB)) & (S::KKEYS - 1u)) * (S::REPK * 8));
-      ev[m] = lds_at<uint2>(lds, vtab_lane + ((xv >> (2 * m * VB)) & (S::VKEYS - 1u)) * (S::REPV * 8));
+    for (int u = 0; u < 2; ++u) {
+      // the word after a row's last one is still staging memory; its bits
+      // land above the 8 * BITS used ones
+      const uint32_t* wk = reinterpret_cast<const uint32_t*>(st + ks_off + u * kStepK);
+      const uint32_t* wv = reinterpret_cast<const uint32_t*>(st + vs_off + u * kStepV);
+      const uint32_t xk = __builtin_amdgcn_alignbit(wk[1], wk[0], ksh);
+      const uint32_t xv = __builtin_amdgcn_alignbit(wv[1], wv[0], vsh);
+      uint2 ek[4], ev[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        ek[m] = lds_at<uint2>(lds, ktab_lane + ((xk >> (2 * m * KB)) & (S::KKEYS - 1u)) * (S::REPK * 8));
+        ev[m] = lds_at<uint2>(lds, vtab_lane + ((xv >> (2 * m * VB)) & (S::VKEYS - 1u)) * (S::REPV * 8));
+      }
+      unsigned char* dk = dc + dk_off + u * kStepDK;
+      unsigned char* dv = dc + dv_off + u * kStepDV;
+      *reinterpret_cast<uint4*>(dk + S::DEC_KHI) = make_uint4(ek[0].x, ek[1].x, ek[2].x, ek[3].x);
+      *reinterpret_cast<uint4*>(dk + S::DEC_KLO) = make_uint4(ek[0].y, ek[1].y, ek[2].y, ek[3].y);
+      *reinterpret_cast<uint4*>(dv + S::DEC_VHI) = make_uint4(ev[0].x, ev[1].x, ev[2].x, ev[3].x);
+      *reinterpret_cast<uint4*>(dv + S::DEC_VLO) = make_uint4(ev[0].y, ev[1].y, ev[2].y, ev[3].y);
     }
-    *reinterpret_cast<uint4*>(dc + S::DEC_KHI + dk_off) = make_uint4(ek[0].x, ek[1].x, ek[2].x, ek[3].x);
-    *reinterpret_cast<uint4*>(dc + S::DEC_KLO + dk_off) = make_uint4(ek[0].y, ek[1].y, ek[2].y, ek[3].y);
-    *reinterpret_cast<uint4*>(dc + S::DEC_VHI + dv_off) = make_uint4(ev[0].x, ev[1].x, ev[2].x, ev[3].x);
-    *reinterpret_cast<uint4*>(dc + S::DEC_VLO + dv_off) = make_uint4(ev[0].y, ev[1].y, ev[2].y, ev[3].y);
     if (tid < 2 * SUB)  // key norms then value norms (staged in that order)
       reinterpret_cast<float*>(dc + S::DEC_KN)[tid] = reinterpret_cast<const float*>(st + S::STG_KN)[tid];
   };
@@ -533,14 +544,15 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
   store_stage(0, 0, rgt);
   if (ntiles > 1) store_stage(1, 1, rg1);
   __syncthreads();
-  decode(0, 0);
+  const bool lead = __builtin_amdgcn_readfirstlane(wave) < kTileNW / 2;
+  if (lead) decode(0, 0);
   __syncthreads();
 
   const bool wave_live = __builtin_amdgcn_readfirstlane(row_w0) < RL;  // wave-uniform
-  // step i (i % 3 == U): load i + 4 into set (i + 1) % 3, decode i + 1
-  // (past the last sub-chunk: stale staging, never read), stage i + 2 from
-  // set (i + 2) % 3.  Waves 0-3 ("lead") then run scores -> softmax -> P V
-  // of sub-chunk i; waves 4-7 ("trail", the other wave on each SIMD) run
+  // step i (i % 3 == U): load i + 4 into set (i + 1) % 3, stage i + 2 from
+  // set (i + 2) % 3.  Waves 0-3 ("lead") run scores -> decode of i + 1 (past
+  // the last sub-chunk: stale staging, never read) -> softmax -> P V of
+  // sub-chunk i; waves 4-7 ("trail", the other wave on each SIMD) run
   // P V of sub-chunk i - 1 -> scores -> softmax of i, so that one wave's
   // vector work tends to meet the other's matrix products rather than its
   // own kind.  A trailing wave keeps sub-chunk i - 1's weights in Ap over
@@ -569,7 +581,6 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
     f32x4_t C[RT][2];
     if (wave_live && i > 0) pv(Prev{}, Ap);
     if (wave_live) scores(Cur{}, C);
-    decode((u + 1) % 3, (u + 1) % 3);
     if (wave_live) softmax(i, Cur{}, C, Ap);
     if (i + 2 < ntiles) store_stage((u + 2) % 3, i + 2, sset);
     __syncthreads();
@@ -577,7 +588,7 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
-  if (__builtin_amdgcn_readfirstlane(wave) < kTileNW / 2) {
+  if (lead) {
 #pragma unroll 1
     for (int i = 0; i < ntiles; i += 3) {
       step_lead(i, I0{}, rg1, rg2);
