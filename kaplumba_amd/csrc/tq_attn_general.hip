@@ -583,62 +583,77 @@ __global__ __launch_bounds__(kGenThreads) void gen_merge_kernel(GenParams p) {
 
 // Partials already in the natural basis (plain values, or the tile kernel's
 // Hadamard values): the merge is element-wise.  Thread = (row, 4 output
-// columns): the splits' (m, l) and o by log-sum-exp, loads in batches of 4
-// splits in flight, / max(l, 1e-6), output in the query dtype.
-__global__ __launch_bounds__(256) void gen_merge_flat_kernel(GenParams p, int64_t n_items) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+// columns): the splits' (m, l) and o by log-sum-exp, / max(l, 1e-6), output
+// in the query dtype.  A split without tokens (m = -inf) has no o written; it is
+// selected away, never multiplied.  Index type I: int when the item count
+// fits, so no 64-bit divisions.
+template <typename I>
+__global__ __launch_bounds__(256) void gen_merge_flat_kernel(GenParams p, I n_items) {
+  const I idx = static_cast<I>(blockIdx.x) * 256 + static_cast<I>(threadIdx.x);
   if (idx >= n_items) return;
   const int C4 = p.Dv / 4;
-  const int RL = p.R * p.L;
+  const I RL = static_cast<I>(p.R) * p.L;
   const int c4 = static_cast<int>(idx % C4);
-  const int64_t row = idx / C4;  // (b * Hkv + gk) * RL + rr
+  const I row = idx / C4;  // (b * Hkv + gk) * RL + rr
   const int rr = static_cast<int>(row % RL);
-  const int64_t bg = row / RL;
+  const I bg = row / RL;
   const int gk = static_cast<int>(bg % p.Hkv);
-  const int64_t b = bg / p.Hkv;
-  const int64_t gi = bg * p.n_rg + rr / 8;
-  const int ri = rr % 8;
+  const I b = bg / p.Hkv;
+  const int64_t gi = static_cast<int64_t>(bg) * p.n_rg + rr / 8;
   const int ns = p.n_splits;
-  float M = -INFINITY, Lsum = 0.f;
+  const int64_t r0 = gi * ns * kGenNQ + rr % 8;  // split k: partial r0 + k * kGenNQ
+  const float2* ml = reinterpret_cast<const float2*>(p.pml) + r0;
+  const float4* po = reinterpret_cast<const float4*>(p.po) + r0 * C4 + c4;
+  const int64_t ostep = static_cast<int64_t>(kGenNQ) * C4;
+  // chunks of 8 splits: every load of a chunk in flight at once, one
+  // rescale of the running sums per chunk
+  float M = -INFINITY;
+  float Lsum = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int k0 = 0; k0 < ns; k0 += 4) {
-    float2 ml[4];
-    float4 oo[4];
+  for (int k0 = 0; k0 < ns; k0 += 8) {
+    float2 m[8];
+    float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = k0 + u;
-      const int64_t r = (gi * ns + k) * kGenNQ + ri;
-      ml[u] = k < ns ? reinterpret_cast<const float2*>(p.pml)[r] : make_float2(-INFINITY, 0.f);
-      oo[u] = (k < ns && ml[u].x != -INFINITY) ? reinterpret_cast<const float4*>(p.po + r * p.Dv)[c4]
-                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u < ns ? k0 + u : k0;  // past the last split: reread one (dropped below)
+      m[u] = ml[k * kGenNQ];
+      v[u] = po[k * ostep];
     }
     float bm = M;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) bm = fmaxf(bm, ml[u].x);
+    for (int u = 0; u < 8; ++u) bm = k0 + u < ns ? fmaxf(bm, m[u].x) : bm;
     if (bm == -INFINITY) continue;
-    const float r0 = M == -INFINITY ? 0.f : expf(M - bm);
-    Lsum *= r0;
-    acc.x *= r0;
-    acc.y *= r0;
-    acc.z *= r0;
-    acc.w *= r0;
+    const float r = M == -INFINITY ? 0.f : expf(M - bm);
+    Lsum *= r;
+    acc.x *= r;
+    acc.y *= r;
+    acc.z *= r;
+    acc.w *= r;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float sc = ml[u].x == -INFINITY ? 0.f : expf(ml[u].x - bm);
-      Lsum = fmaf(sc, ml[u].y, Lsum);
-      acc.x = fmaf(sc, oo[u].x, acc.x);
-      acc.y = fmaf(sc, oo[u].y, acc.y);
-      acc.z = fmaf(sc, oo[u].z, acc.z);
-      acc.w = fmaf(sc, oo[u].w, acc.w);
+    for (int u = 0; u < 8; ++u) {
+      const bool live = k0 + u < ns && m[u].x != -INFINITY;
+      const float sc = live ? expf(m[u].x - bm) : 0.f;
+      Lsum = fmaf(sc, m[u].y, Lsum);
+      acc.x = live ? fmaf(sc, v[u].x, acc.x) : acc.x;
+      acc.y = live ? fmaf(sc, v[u].y, acc.y) : acc.y;
+      acc.z = live ? fmaf(sc, v[u].z, acc.z) : acc.z;
+      acc.w = live ? fmaf(sc, v[u].w, acc.w) : acc.w;
     }
     M = bm;
   }
   const float inv = M == -INFINITY ? 0.f : 1.f / fmaxf(Lsum, kNormEps);
-  const int64_t o = ((b * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L) * p.Dv + 4 * c4;
-  store_out(p.out, p.q_dtype, o, acc.x * inv);
-  store_out(p.out, p.q_dtype, o + 1, acc.y * inv);
-  store_out(p.out, p.q_dtype, o + 2, acc.z * inv);
-  store_out(p.out, p.q_dtype, o + 3, acc.w * inv);
+  const int64_t o = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L) * p.Dv + 4 * c4;
+  const float v0 = acc.x * inv, v1 = acc.y * inv, v2 = acc.z * inv, v3 = acc.w * inv;
+  if (p.q_dtype == TQ_DTYPE_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p.out) + o) = make_float4(v0, v1, v2, v3);
+  } else {
+    const bool f16 = p.q_dtype == TQ_DTYPE_F16;
+    const uint32_t a = f16 ? (f32_to_f16_bits(v0) | (static_cast<uint32_t>(f32_to_f16_bits(v1)) << 16))
+                           : (f32_to_bf16_bits(v0) | (static_cast<uint32_t>(f32_to_bf16_bits(v1)) << 16));
+    const uint32_t c = f16 ? (f32_to_f16_bits(v2) | (static_cast<uint32_t>(f32_to_f16_bits(v3)) << 16))
+                           : (f32_to_bf16_bits(v2) | (static_cast<uint32_t>(f32_to_bf16_bits(v3)) << 16));
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + o) = make_uint2(a, c);
+  }
 }
 
 // --------------------------------------------------------------- launch ---
@@ -977,8 +992,11 @@ int general_attention(const GenCall& c) {
   if (rc) return rc;
   if (plain || p.po_natural) {
     const int64_t items = static_cast<int64_t>(c.B) * c.Hkv * (c.Hq / c.Hkv) * c.L * (c.Dv / 4);
-    hipLaunchKernelGGL(gen_merge_flat_kernel, dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), 0, st,
-                       p, items);
+    const dim3 fgrid(static_cast<unsigned>((items + 255) / 256));
+    if (items < (int64_t(1) << 31) - 256)
+      hipLaunchKernelGGL(gen_merge_flat_kernel<int>, fgrid, dim3(256), 0, st, p, static_cast<int>(items));
+    else
+      hipLaunchKernelGGL(gen_merge_flat_kernel<int64_t>, fgrid, dim3(256), 0, st, p, items);
     return check_launch("gen_merge_flat_kernel");
   }
   const unsigned zc = (!plain && c.v_rot_kind == TQ_ROT_DENSE) ? static_cast<unsigned>((c.Dv + 63) / 64) : 1u;
