@@ -204,8 +204,15 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     }
   };
 
-  // ---- prologue loads first (this wave's two query rows, signs, codebooks),
-  // then the pipeline's sub-chunks (loads complete in order)
+  float ckb[1 << KB], cvb[1 << VB];
+#pragma unroll
+  for (int i = 0; i < (1 << KB); ++i) ckb[i] = p.kcb[i];
+#pragma unroll
+  for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
+  // ---- prologue: the codebooks first, then this wave's two query rows and
+  // the signs; the pair tables are built before the pipeline's sub-chunks are
+  // requested, so that waiting for the codebooks never waits for the
+  // sub-chunks behind them (loads complete in order)
   uint32_t qraw[2][QE];
   float sgn[QE];
   {
@@ -228,11 +235,6 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
 #pragma unroll
     for (int e = 0; e < QE; ++e) sgn[e] = dense ? 1.f : p.krot[lane + e * kWave];
   }
-  float ckb[1 << KB], cvb[1 << VB];
-#pragma unroll
-  for (int i = 0; i < (1 << KB); ++i) ckb[i] = p.kcb[i];
-#pragma unroll
-  for (int i = 0; i < (1 << VB); ++i) cvb[i] = p.vcb[i];
   // f16 norms with an odd slab end: the last token's norms are read with
   // 2-byte loads (the 16-byte load reads the dword that also spans token
   // t_end as zero) and patched in its sub-chunk's slow path
@@ -243,14 +245,8 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     tail_k = __builtin_amdgcn_raw_buffer_load_b16(knrs, off, 0, 0);
     tail_v = __builtin_amdgcn_raw_buffer_load_b16(vnrs, off, 0, 0);
   }
-  Buf buf[P];
-#pragma unroll
-  for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
-
   // ---- pair tables (as in the small kernel): keys as hi and lo tables of
-  // 4-byte entries, values as (hi pair, lo pair) entries; values from the
-  // scalar codebook copies, since vector loads here would wait for the
-  // prefetch above
+  // 4-byte entries, values as (hi pair, lo pair) entries
   float kmax = 0.f, vmax = 0.f;
 #pragma unroll
   for (int i = 0; i < (1 << KB); ++i) kmax = fmaxf(kmax, fabsf(ckb[i]));
@@ -284,6 +280,10 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
       d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
     }
   }
+
+  Buf buf[P];
+#pragma unroll
+  for (int s = 0; s < P; ++s) load_sub(buf[s], sub_start(s));
 
   // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
   // (dense: rotated by qprep_kernel), into LDS with each row's max |y|
