@@ -48,10 +48,12 @@ __global__ __launch_bounds__(kQprepThreads) void qprep_kernel(AttnParams p, int6
     const int64_t row = row0 + r;  // (b*Hq + h)*L + l
     float v[SEG];
     if (row < n_rows) {
-      const int l = static_cast<int>(row % p.L);
-      const int64_t bh = row / p.L;
-      const int h = static_cast<int>(bh % p.Hq);
-      const int b = static_cast<int>(bh / p.Hq);
+      // 32-bit index math (tq_attention rejects 2^31 rows or more)
+      const int row32 = static_cast<int>(row);
+      const int l = row32 % p.L;
+      const int bh = row32 / p.L;
+      const int h = bh % p.Hq;
+      const int b = bh / p.Hq;
       const int64_t base = b * p.q_sb + h * p.q_sh + l * p.q_sl + j0;
 #pragma unroll
       for (int e = 0; e < SEG; ++e) v[e] = load_elem<QDT>(p.q, base + e);
@@ -367,6 +369,8 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   p.n_rg = sp.n_rg;
   p.nq = sp.nq;
   const int64_t rows = static_cast<int64_t>(B) * Hq * L;
+  if (rows >= (int64_t(1) << 31))
+    return fail(TQ_ERR_UNSUPPORTED, "attention: %lld query rows", static_cast<long long>(rows));
   char* ws = static_cast<char*>(workspace);
   p.qrot = reinterpret_cast<float*>(ws);
   ws += (rows * dim * 4 + 255) / 256 * 256;
