@@ -91,7 +91,8 @@ struct GenParams {
   float* pml;    // [B*Hkv*n_rg, n_splits, 8, 2]
   float rscale_k, rscale_v;  // f32(1/sqrt(Dk)), f32(1/sqrt(Dv))
   float qjl_scale;           // f32(sqrt(pi/2) / Dk)
-  int po_natural;            // partials already through R_V^-1 (the tile kernel, Hadamard values)
+  int po_natural;            // partials already in the natural value basis (plain values)
+  int merge_had;             // the element-wise merge applies R_V^-1 (Hadamard) per merged row
   uint32_t* qhl;             // tile kernel: per query row, q_rot * sq as hi then lo f16 [rows, 2, Dk / 2] u32
   float* qsq;                // tile kernel: sq per query row
   void* out;                 // [B, Hq, L, Dv] in the query dtype

@@ -581,10 +581,14 @@ __global__ __launch_bounds__(kGenThreads) void gen_merge_kernel(GenParams p) {
   }
 }
 
-// Partials already in the natural basis (plain values, or the tile kernel's
-// Hadamard values): the merge is element-wise.  Thread = (row, 4 output
-// columns): the splits' (m, l) and o by log-sum-exp, / max(l, 1e-6), output
-// in the query dtype.  A split without tokens (m = -inf) has no o written; it is
+// Element-wise merge: partials in the natural basis (plain values), or the
+// tile kernel's Hadamard-rotated ones (merge_had, Dv = 128).  Thread = (row,
+// 4 output columns): the splits' (m, l) and o by log-sum-exp, / max(l,
+// 1e-6); for merge_had then R_V^-1 on the merged row (the 32 threads of a
+// row are 32 consecutive lanes: butterflies over the 4 columns in registers,
+// over column bits 2-6 across lanes, then the signs and 1/sqrt(Dv), the
+// order of _rht_inverse, turboquant_cache.py:3564-3575); output in the
+// query dtype.  A split without tokens (m = -inf) has no o written; it is
 // selected away, never multiplied.  Index type I: int when the item count
 // fits, so no 64-bit divisions.
 template <typename I>
@@ -643,7 +647,35 @@ __global__ __launch_bounds__(256) void gen_merge_flat_kernel(GenParams p, I n_it
   }
   const float inv = M == -INFINITY ? 0.f : 1.f / fmaxf(Lsum, kNormEps);
   const int64_t o = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + rr / p.L) * p.L + rr % p.L) * p.Dv + 4 * c4;
-  const float v0 = acc.x * inv, v1 = acc.y * inv, v2 = acc.z * inv, v3 = acc.w * inv;
+  float v0 = acc.x * inv, v1 = acc.y * inv, v2 = acc.z * inv, v3 = acc.w * inv;
+  if (p.merge_had) {
+    const float a0 = v0 + v1, a1 = v0 - v1, a2 = v2 + v3, a3 = v2 - v3;
+    v0 = a0 + a2;
+    v2 = a0 - a2;
+    v1 = a1 + a3;
+    v3 = a1 - a3;
+    float o;
+#define TQ_MERGE_STAGE(HB)                 \
+  o = xor_lane<HB>(v0);                    \
+  v0 = (c4 & HB) ? o - v0 : v0 + o;        \
+  o = xor_lane<HB>(v1);                    \
+  v1 = (c4 & HB) ? o - v1 : v1 + o;        \
+  o = xor_lane<HB>(v2);                    \
+  v2 = (c4 & HB) ? o - v2 : v2 + o;        \
+  o = xor_lane<HB>(v3);                    \
+  v3 = (c4 & HB) ? o - v3 : v3 + o;
+    TQ_MERGE_STAGE(1)
+    TQ_MERGE_STAGE(2)
+    TQ_MERGE_STAGE(4)
+    TQ_MERGE_STAGE(8)
+    TQ_MERGE_STAGE(16)
+#undef TQ_MERGE_STAGE
+    const float4 sg = reinterpret_cast<const float4*>(p.vrot)[c4];
+    v0 *= sg.x * p.rscale_v;
+    v1 *= sg.y * p.rscale_v;
+    v2 *= sg.z * p.rscale_v;
+    v3 *= sg.w * p.rscale_v;
+  }
   if (p.q_dtype == TQ_DTYPE_F32) {
     *reinterpret_cast<float4*>(static_cast<float*>(p.out) + o) = make_float4(v0, v1, v2, v3);
   } else {
@@ -967,9 +999,10 @@ int general_attention(const GenCall& c) {
 
   hipStream_t st = static_cast<hipStream_t>(c.stream);
   // the tile kernel takes its query rows split per row (gen_tile_qprep_kernel,
-  // which rotates Hadamard queries itself) and hands over natural-basis
-  // partials for Hadamard values
-  p.po_natural = (tile && c.v_rot_kind == TQ_ROT_HADAMARD) ? 1 : 0;
+  // which rotates Hadamard queries itself); its Hadamard-rotated partials go
+  // to the element-wise merge, which applies R_V^-1 once per row
+  p.po_natural = plain ? 1 : 0;
+  p.merge_had = (tile && c.v_rot_kind == TQ_ROT_HADAMARD) ? 1 : 0;
   if (plain)
     launch_qprep_mode(p, rows, 0, nullptr, p.qrot, st);
   else if (tile && c.k_rot_kind == TQ_ROT_HADAMARD)
@@ -990,7 +1023,7 @@ int general_attention(const GenCall& c) {
   }
   rc = tile ? launch_tile_partial(p, kb, c.v_bits, st) : launch_gen_partial(p, kb, plain ? 0 : c.v_bits, st);
   if (rc) return rc;
-  if (plain || p.po_natural) {
+  if (plain || p.merge_had) {
     const int64_t items = static_cast<int64_t>(c.B) * c.Hkv * (c.Hq / c.Hkv) * c.L * (c.Dv / 4);
     const dim3 fgrid(static_cast<unsigned>((items + 255) / 256));
     if (items < (int64_t(1) << 31) - 256)

@@ -32,9 +32,8 @@
 //           coordinate), hi and lo parts;
 //   stage   sub-chunk i + 2's registers into its LDS staging slot.
 // Queries arrive prepared per row by gen_tile_qprep_kernel (below).
-// Output: (o, max, sum) per row in the general path's 8-row partial layout;
-// for Hadamard values o already passed through R_V^-1 (butterflies over
-// registers and lanes), otherwise in the rotated basis.  Scores are
+// Output: (o, max, sum) per row in the general path's 8-row partial layout,
+// o in the rotated value basis (the merge applies R_V^-1 once per row).  Scores are
 // s_t = n_t <q_rot, c[idx_t]>, values n_t c[idx_t] (quantized_attention,
 // turboquant_cache.py:5110-5203); the causal rule, ragged lengths and left
 // padding as in the general path; no array mask (those take gen_partial_kernel).
@@ -626,42 +625,7 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
       pm[1] = lr;
     }
   }
-  float osc = ldexpf(1.f, E) / sv;
-  if (p.v_rot_kind == TQ_ROT_HADAMARD) {
-    // R_V^-1 on the partial (linear, so the merge sees natural-basis rows):
-    // coordinate 16 ct + n: butterflies over ct in registers, n across lanes
-    float vr[8];
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) vr[ct] = p.vrot[16 * ct + n];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-#pragma unroll
-        for (int hb = 1; hb < 8; hb <<= 1)
-#pragma unroll
-          for (int ct = 0; ct < 8; ++ct)
-            if ((ct & hb) == 0) {
-              const float a0 = O[rt][ct][k], a1 = O[rt][ct + hb][k];
-              O[rt][ct][k] = a0 + a1;
-              O[rt][ct + hb][k] = a0 - a1;
-            }
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct) {
-          float v = O[rt][ct][k];
-          float o = xor_lane<1>(v);
-          v = (n & 1) ? o - v : v + o;
-          o = xor_lane<2>(v);
-          v = (n & 2) ? o - v : v + o;
-          o = xor_lane<4>(v);
-          v = (n & 4) ? o - v : v + o;
-          o = xor_lane<8>(v);
-          v = (n & 8) ? o - v : v + o;
-          O[rt][ct][k] = v * vr[ct];
-        }
-      }
-    osc *= p.rscale_v;
-  }
+  const float osc = ldexpf(1.f, E) / sv;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
