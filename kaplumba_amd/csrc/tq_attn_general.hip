@@ -1015,7 +1015,7 @@ int general_attention(const GenCall& c) {
   int rc = check_launch("gen_qprep_kernel");
   if (rc) return rc;
   if (tile) {
-    const int64_t wgs = (rows + 63) / 64;
+    const int64_t wgs = (rows + kTileQpRows * (kTileQpThreads / 64) - 1) / (kTileQpRows * (kTileQpThreads / 64));
     hipLaunchKernelGGL(gen_tile_qprep_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kTileQpThreads), 0, st, p,
                        static_cast<int>(rows));
     rc = check_launch("gen_tile_qprep_kernel");

@@ -638,27 +638,27 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
     }
 }
 
-// Coordinates 32 s + 8 g + j (register 8 s + j) of one query row from element
-// offset qo (lane group g's first coordinate): round_DT(q * scale) times the
+// Coordinates 16 g8 + j (register j) of one query row from element offset
+// qo (lane group g8's first coordinate): round_DT(q * scale) times the
 // Hadamard signs, all loads issued before the first use.
 template <int DT>
-__device__ __forceinline__ void tile_q_signed(const void* q, int64_t qo, float scale, const float (&kr)[32],
-                                              float (&qv)[32]) {
+__device__ __forceinline__ void tile_q_signed(const void* q, int64_t qo, float scale, const float (&kr)[16],
+                                              float (&qv)[16]) {
   if constexpr (DT == TQ_DTYPE_F32) {
     const float* qp = static_cast<const float*>(q) + qo;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) qv[e] = qp[32 * (e >> 3) + (e & 7)];
+    for (int e = 0; e < 16; ++e) qv[e] = qp[e];
   } else {
     const uint16_t* qp = static_cast<const uint16_t*>(q) + qo;
-    uint16_t raw[32];
+    uint16_t raw[16];
 #pragma unroll
-    for (int e = 0; e < 32; ++e) raw[e] = qp[32 * (e >> 3) + (e & 7)];
+    for (int e = 0; e < 16; ++e) raw[e] = qp[e];
 #pragma unroll
-    for (int e = 0; e < 32; ++e)
+    for (int e = 0; e < 16; ++e)
       qv[e] = DT == TQ_DTYPE_F16 ? f16_bits_to_f32(raw[e]) : bf16_bits_to_f32(raw[e]);
   }
 #pragma unroll
-  for (int e = 0; e < 32; ++e) qv[e] = round_to<DT>(qv[e] * scale) * kr[e];
+  for (int e = 0; e < 16; ++e) qv[e] = round_to<DT>(qv[e] * scale) * kr[e];
 }
 
 // Query rows for the tile kernel, once per row rather than once per split:
@@ -666,63 +666,68 @@ __device__ __forceinline__ void tile_q_signed(const void* q, int64_t qo, float s
 // workspace), times sq (a power of two putting the row's largest magnitude
 // in [2^12, 2^13)), split into hi and lo f16 parts and stored in the order
 // the tile kernel's B operands take them: row-major, per row 16 hi words of
-// 8 halves (coordinate group s, lane group g at word 4 s + g), then 16 lo.
-// Wave = 16 consecutive query rows, lane (row n, g) holds coordinates
-// 32 s + 8 g + j in register 8 s + j (butterflies over coordinate bits 0-2
-// and 5-6 in registers, bits 3-4 across lanes).
+// 8 halves (word 4 s + g holds coordinates 32 s + 8 g .. + 7), then 16 lo.
+// Wave = 8 consecutive query rows, lane (row n8 = lane % 8, g8 = lane / 8)
+// holds coordinates 16 g8 + j in register j: butterflies over coordinate
+// bits 0-3 in registers, bits 4-6 across lanes (lane bits 3-5).  A lane
+// stores words 2 g8, 2 g8 + 1 of both halves (32 contiguous bytes each).
 constexpr int kTileQpThreads = 256;
+constexpr int kTileQpRows = 8;  // query rows per wave
 
 __global__ __launch_bounds__(kTileQpThreads) void gen_tile_qprep_kernel(GenParams p, int rows) {
   const int lane = threadIdx.x & 63;
-  const int n = lane & 15;
-  const int g = lane >> 4;
-  const int row0 = (blockIdx.x * (kTileQpThreads / 64) + (threadIdx.x >> 6)) * 16;
+  const int n8 = lane & 7;
+  const int g8 = lane >> 3;
+  const int row0 = (blockIdx.x * (kTileQpThreads / 64) + (threadIdx.x >> 6)) * kTileQpRows;
   if (__builtin_amdgcn_readfirstlane(row0) >= rows) return;  // whole wave past the end
-  const int row = row0 + n;
+  const int row = row0 + n8;
   const bool ok = row < rows;
   const int qrow = ok ? row : 0;
-  float qv[32];
+  float qv[16];
   if (p.k_rot_kind == TQ_ROT_HADAMARD) {
-    float kr[32];
+    float kr[16];
 #pragma unroll
-    for (int e = 0; e < 32; ++e) kr[e] = p.krot[32 * (e >> 3) + 8 * g + (e & 7)];
+    for (int e = 0; e < 16; ++e) kr[e] = p.krot[16 * g8 + e];
     const int l = qrow % p.L;
     const int bh = qrow / p.L;
     const int h = bh % p.Hq;
     const int b = bh / p.Hq;
     const int64_t qo = static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(h) * p.q_sh +
-                       static_cast<int64_t>(l) * p.q_sl + 8 * g;
+                       static_cast<int64_t>(l) * p.q_sl + 16 * g8;
     switch (p.q_dtype) {
       case TQ_DTYPE_F32: tile_q_signed<TQ_DTYPE_F32>(p.q, qo, p.scale_q, kr, qv); break;
       case TQ_DTYPE_F16: tile_q_signed<TQ_DTYPE_F16>(p.q, qo, p.scale_q, kr, qv); break;
       default: tile_q_signed<TQ_DTYPE_BF16>(p.q, qo, p.scale_q, kr, qv); break;
     }
 #pragma unroll
-    for (int hb = 1; hb < 32; hb <<= 1)
+    for (int hb = 1; hb < 16; hb <<= 1)
 #pragma unroll
-      for (int e = 0; e < 32; ++e)
+      for (int e = 0; e < 16; ++e)
         if ((e & hb) == 0) {
           const float a0 = qv[e], a1 = qv[e + hb];
           qv[e] = a0 + a1;
           qv[e + hb] = a0 - a1;
         }
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
+    for (int e = 0; e < 16; ++e) {
       float v = qv[e];
-      const float o16 = xor_lane<16>(v);
-      v = (g & 1) ? o16 - v : v + o16;
+      float o = xor_lane<8>(v);
+      v = (g8 & 1) ? o - v : v + o;
+      o = xor_lane<16>(v);
+      v = (g8 & 2) ? o - v : v + o;
       const float2 hv = halves(v);  // lanes < 32: (v, v[l + 32]); others (v[l - 32], v)
-      v = (g & 2) ? hv.x - hv.y : hv.x + hv.y;
+      v = (g8 & 4) ? hv.x - hv.y : hv.x + hv.y;
       qv[e] = v * p.rscale_k;
     }
   } else {
-    const float* qp = p.qrot + static_cast<int64_t>(qrow) * p.DkP + 8 * g;
+    const float* qp = p.qrot + static_cast<int64_t>(qrow) * p.DkP + 16 * g8;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) qv[e] = qp[32 * (e >> 3) + (e & 7)];
+    for (int e = 0; e < 16; ++e) qv[e] = qp[e];
   }
   float mx = 0.f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) mx = fmaxf(mx, fabsf(qv[e]));
+  for (int e = 0; e < 16; ++e) mx = fmaxf(mx, fabsf(qv[e]));
+  mx = fmaxf(mx, xor_lane<8>(mx));
   mx = fmaxf(mx, xor_lane<16>(mx));
   {
     const float2 hv = halves(mx);
@@ -730,22 +735,22 @@ __global__ __launch_bounds__(kTileQpThreads) void gen_tile_qprep_kernel(GenParam
   }
   const float sq = f16_split_scale(mx);
   if (!ok) return;
-  u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.qhl) + static_cast<int64_t>(row) * 32 + g;
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.qhl) + static_cast<int64_t>(row) * 32 + 2 * g8;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int w = 0; w < 2; ++w) {
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t h0, l0, h1, l1;
-      split_f16(qv[8 * s + 2 * j] * sq, h0, l0);
-      split_f16(qv[8 * s + 2 * j + 1] * sq, h1, l1);
+      split_f16(qv[8 * w + 2 * j] * sq, h0, l0);
+      split_f16(qv[8 * w + 2 * j + 1] * sq, h1, l1);
       hw[j] = h0 | (h1 << 16);
       lw[j] = l0 | (l1 << 16);
     }
-    dst[4 * s] = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
-    dst[16 + 4 * s] = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+    dst[w] = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+    dst[16 + w] = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
   }
-  if (g == 0) p.qsq[row] = sq;
+  if (g8 == 0) p.qsq[row] = sq;
 }
 
 }  // namespace tq
