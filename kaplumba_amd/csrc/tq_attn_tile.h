@@ -16,8 +16,8 @@
 //           products.  The two 16-token tiles hold tokens 8 (m / 4) + 4 h +
 //           m % 4 in row m of tile h, so lane (row n, g) ends with tokens
 //           8 g .. 8 g + 7;
-//   decode  sub-chunk i + 1, by the four lead waves after their score
-//           products: thread (token, 8 coordinates) looks up the K and V
+//   decode  sub-chunk i + 1, by the four lead waves between their softmax
+//           and their P V: thread (token, 8 coordinates) looks up the K and V
 //           pair tables and writes 16 bytes each of the hi and lo f16 parts
 //           of the scaled codebook values; K rows go to the slot the score
 //           MFMA reads them from, V rows into 16-column blocks (32 bytes per
@@ -549,8 +549,8 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
 
   const bool wave_live = __builtin_amdgcn_readfirstlane(row_w0) < RL;  // wave-uniform
   // step i (i % 3 == U): load i + 4 into set (i + 1) % 3, stage i + 2 from
-  // set (i + 2) % 3.  Waves 0-3 ("lead") run scores -> decode of i + 1 (past
-  // the last sub-chunk: stale staging, never read) -> softmax -> P V of
+  // set (i + 2) % 3.  Waves 0-3 ("lead") run scores -> softmax -> decode of
+  // i + 1 (past the last sub-chunk: stale staging, never read) -> P V of
   // sub-chunk i; waves 4-7 ("trail", the other wave on each SIMD) run
   // P V of sub-chunk i - 1 -> scores -> softmax of i, so that one wave's
   // vector work tends to meet the other's matrix products rather than its
@@ -562,12 +562,12 @@ __global__ __launch_bounds__(kTileThreads) void gen_tile_kernel(GenParams p, int
     if (i + 4 < ntiles) load_tile(i + 4, lset);
     f32x4_t C[RT][2];
     u32x4_t A[RT];
-    if (wave_live) scores(Cur{}, C);
-    decode((u + 1) % 3, (u + 1) % 3);
     if (wave_live) {
+      scores(Cur{}, C);
       softmax(i, Cur{}, C, A);
-      pv(Cur{}, A);
     }
+    decode((u + 1) % 3, (u + 1) % 3);
+    if (wave_live) pv(Cur{}, A);
     if (i + 2 < ntiles) store_stage((u + 2) % 3, i + 2, sset);
     __syncthreads();
   };
