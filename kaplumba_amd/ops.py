@@ -19,6 +19,18 @@ from . import codebook as cbmod
 ROTATIONS = {"hadamard": _lib.TQ_ROT_HADAMARD, "dense": _lib.TQ_ROT_DENSE}
 
 
+def _fields(c: "Codec") -> tuple:
+    """A codec's defining fields, as the torch.ops.kaplumba operators take them."""
+    return (c.dim, c.bits, c.seed, c.rotation, c.codebook_kind)
+
+
+def _opt_tensor(x, dtype):
+    """None, a tensor, or x as a tensor (lists and arrays of lengths, starts or masks)."""
+    if x is None or isinstance(x, torch.Tensor):
+        return x
+    return torch.as_tensor(np.asarray(x), dtype=dtype)
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -84,11 +96,13 @@ class Codec:
 
 
 def append_quantize(x: torch.Tensor, codec: Codec, packed: torch.Tensor, norms: torch.Tensor,
-                    offset: int) -> None:
+                    offset: int, _direct: bool = False) -> None:
     """Quantize x (B, H, L, D) into rows offset..offset+L of the capacity buffers.
 
     packed: (B, H, cap, PW) uint32 contiguous; norms: (B, H, cap) f32/f16 contiguous.
     """
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.append_quantize(x, packed, norms, offset, *_fields(codec))
     _require_device(x, packed, norms)
     x = _check_append_buffers(x, codec, packed, norms)
     B, H, L, D = x.shape
@@ -126,18 +140,22 @@ def _check_append_buffers(x: torch.Tensor, codec: Codec, packed: torch.Tensor,
 
 def append_quantize_kv(k: torch.Tensor, v: torch.Tensor, key_codec: Codec, value_codec: Codec,
                        k_packed: torch.Tensor, k_norms: torch.Tensor, v_packed: torch.Tensor,
-                       v_norms: torch.Tensor, offset: int) -> None:
+                       v_norms: torch.Tensor, offset: int, _direct: bool = False) -> None:
     """Quantize keys and values (B, H, L, D) of one append in one library call.
 
     Both sides share shape, dtype, rotation kind, norm dtype and capacity;
     anything else goes through two append_quantize calls.
     """
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.append_quantize_kv(k, v, k_packed, k_norms, v_packed, v_norms,
+                                                     offset, *_fields(key_codec),
+                                                     *_fields(value_codec))
     same = (k.shape == v.shape and k.dtype == v.dtype and key_codec.dim == value_codec.dim
             and key_codec.rot_kind == value_codec.rot_kind and k_norms.dtype == v_norms.dtype
             and k_packed.shape[2] == v_packed.shape[2])
     if not same:
-        append_quantize(k, key_codec, k_packed, k_norms, offset)
-        append_quantize(v, value_codec, v_packed, v_norms, offset)
+        append_quantize(k, key_codec, k_packed, k_norms, offset, _direct=True)
+        append_quantize(v, value_codec, v_packed, v_norms, offset, _direct=True)
         return
     _require_device(k, v, k_packed, k_norms, v_packed, v_norms)
     k = _check_append_buffers(k, key_codec, k_packed, k_norms)
@@ -154,8 +172,10 @@ def append_quantize_kv(k: torch.Tensor, v: torch.Tensor, key_codec: Codec, value
     _lib.check(rc, "tq_append_quantize_kv")
 
 
-def append_plain(x: torch.Tensor, dst: torch.Tensor, offset: int) -> None:
+def append_plain(x: torch.Tensor, dst: torch.Tensor, offset: int, _direct: bool = False) -> None:
     """Copy x (B, H, L, D) into rows offset.. of dst (B, H, cap, D) (fp16/bf16)."""
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.append_plain(x, dst, offset)
     _require_device(x, dst)
     B, H, L, D = x.shape
     if x.dtype != dst.dtype:
@@ -197,8 +217,11 @@ def _capacity_of(norms: torch.Tensor, indices: torch.Tensor, pw: int) -> int:
     return cap
 
 
-def dequantize(indices: torch.Tensor, norms: torch.Tensor, codec: Codec) -> torch.Tensor:
+def dequantize(indices: torch.Tensor, norms: torch.Tensor, codec: Codec,
+               _direct: bool = False) -> torch.Tensor:
     """f32 (B, H, T, D) reconstruction n * R^-1(codebook[idx])."""
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.dequantize(indices, norms, *_fields(codec))
     _require_device(indices, norms)
     B, H, T = norms.shape
     out = torch.empty((B, H, T, codec.dim), dtype=torch.float32, device=norms.device)
@@ -354,7 +377,8 @@ def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.
                      v_norms: torch.Tensor, v_idx: torch.Tensor, key_codec: Codec,
                      value_codec: Codec, scale: float, causal: bool,
                      seq_lens: Optional[torch.Tensor] = None,
-                     seq_starts: Optional[torch.Tensor] = None, mask=None) -> torch.Tensor:
+                     seq_starts: Optional[torch.Tensor] = None, mask=None,
+                     _direct: bool = False) -> torch.Tensor:
     """Attention straight from packed K/V state views (B, Hkv, T[, PW]).
 
     ``seq_lens`` (B,) ends each sequence before T (ragged batches);
@@ -363,6 +387,11 @@ def attention_packed(queries: torch.Tensor, k_norms: torch.Tensor, k_idx: torch.
     in head dim and rotation; the output has the value dim
     (turboquant_cache.py:5131).
     """
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.attention_packed(
+            queries, k_norms, k_idx, v_norms, v_idx, *_fields(key_codec), *_fields(value_codec),
+            float(scale), bool(causal), _opt_tensor(seq_lens, torch.int32),
+            _opt_tensor(seq_starts, torch.int32), _opt_tensor(mask, None))
     _require_device(queries, k_norms, k_idx, v_norms, v_idx)
     B, Hq, L, D = queries.shape
     Hkv, T = k_norms.shape[1], k_norms.shape[2]
@@ -426,7 +455,8 @@ def _plain_capacity(t: torch.Tensor) -> int:
 def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                     scale: float, causal: bool,
                     seq_lens: Optional[torch.Tensor] = None,
-                    seq_starts: Optional[torch.Tensor] = None, mask=None) -> torch.Tensor:
+                    seq_starts: Optional[torch.Tensor] = None, mask=None,
+                    _direct: bool = False) -> torch.Tensor:
     """Attention over unquantized fp16/bf16 K/V views (B, Hkv, T, Dk / Dv) of
     (B, Hkv, cap, D) buffers.
 
@@ -434,6 +464,11 @@ def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Ten
     array mask broadcast as the fp16 layers' SDPA does (against
     (B, Hq, L, T), base.py:218-226).
     """
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.attention_plain(
+            queries, keys, values, float(scale), bool(causal),
+            _opt_tensor(seq_lens, torch.int32), _opt_tensor(seq_starts, torch.int32),
+            _opt_tensor(mask, None))
     _require_device(queries, keys, values)
     B, Hq, L, D = queries.shape
     Hkv, T = keys.shape[1], keys.shape[2]
@@ -473,3 +508,7 @@ def attention_plain(queries: torch.Tensor, keys: torch.Tensor, values: torch.Ten
     tail = (1 if causal else 0, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(queries))
     _call_attention(lib, head, seq_starts, seq_lens, tail, "tq_attention(plain)")
     return out
+
+
+# Registers torch.ops.kaplumba.* (they call back into the functions above).
+from . import torch_ops  # noqa: E402,F401

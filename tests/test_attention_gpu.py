@@ -172,6 +172,19 @@ def test_query_dtypes_and_f16_norms(device, qdt):
     run_case(device, 5, 2, 8, 2, 1, 600, 128, 3, 3, qdt=qdt, norm="float16")
 
 
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 1), (1, 2), (2, 2)])
+@pytest.mark.parametrize("Hq,Hkv,L,T,qdt,norm", [
+    (16, 8, 1, 2500, "bf16", "float32"),   # two rows per kv head, several splits
+    (8, 2, 1, 300, "f32", "float16"),      # four rows, one split (finished in the kernel)
+    (4, 2, 2, 1234, "f16", "float32"),     # two causal verify rows per head
+])
+def test_d256_dense_row_groups(device, kb, vb, Hq, Hkv, L, T, qdt, norm):
+    """d = 256, dense rotation, <= 4 rows per kv head and 1- or 2-bit values: the staged
+    row-group kernel, for every key width."""
+    run_case(device, 300 + 10 * kb + vb + L, 2, Hq, Hkv, L, T, 256, kb, vb, rot="dense",
+             qdt=qdt, norm=norm)
+
+
 def test_ragged_batch_dense_d256(device):
     """Config-2 shape at reduced size: ragged lengths, d=256, K4/V2, dense rotation."""
     lengths = [300, 1, 1700, 0, 999]
