@@ -71,6 +71,10 @@ class _QuantizedStateProxy:
         self.shape = (batch, n_heads, n_tokens, head_dim)
 
     def __getattr__(self, name):
+        # only names the slots do not hold get here; an unset slot (an object
+        # under construction or being copied) is missing, not forwarded
+        if name in _QuantizedStateProxy.__slots__:
+            raise AttributeError(name)
         return getattr(self._state, name)
 
     def __iter__(self):

@@ -227,3 +227,20 @@ def test_save_load_keeps_codec_options():
     assert r.key_codec.packed_width == r.state[0].indices.shape[-1]
     assert r.value_codec.packed_width == r.state[1].indices.shape[-1]
     assert torch.equal(r.state[0].indices, c.state[0].indices)
+
+
+def test_state_proxy_copies_and_forwards():
+    """The (B, H, T, D) state proxy forwards attributes to its state and can be
+    copied (a copy reads the slots before they are set: no recursion)."""
+    import copy
+
+    from kaplumba_amd.cache import TurboQuantMSEState, _QuantizedStateProxy
+
+    st = TurboQuantMSEState(torch.zeros(1, 2, 8), torch.zeros(1, 2, 8, 12, dtype=torch.int32))
+    p = _QuantizedStateProxy(st, 5, 2, 128, 1)
+    assert p.shape == (1, 2, 5, 128) and p.norms is st.norms
+    q = copy.copy(p)
+    assert q.shape == p.shape and q.indices is st.indices
+    blank = _QuantizedStateProxy.__new__(_QuantizedStateProxy)
+    with pytest.raises(AttributeError):
+        blank._state

@@ -115,3 +115,30 @@ def test_opcheck_every_operator(device):
     mask = torch.ones(2, T, dtype=torch.bool, device=device).tril(T - 2)
     torch.library.opcheck(torch.ops.kaplumba.attention_plain.default,
                           (q, plain[:, :, :T], plain[:, :, :T], 0.125, False, None, None, mask))
+
+
+@pytest.mark.parametrize("bits", [3, 3.5])
+def test_compiled_cache_layer_matches_eager(device, bits):
+    """A model layer's cache calls (update_and_fetch, then the SDPA dispatch) under
+    torch.compile: prefill, cache growth and decode steps give the eager bits."""
+    from kaplumba_amd import TurboQuantKVCache, scaled_dot_product_attention
+
+    torch._dynamo.reset()
+
+    def layer(cache, q, k, v):
+        ks, vs = cache.update_and_fetch(k, v)
+        mask = "causal" if q.shape[2] > 1 else None
+        return scaled_dot_product_attention(q, ks, vs, cache, 1 / math.sqrt(q.shape[-1]), mask)
+
+    g = torch.Generator(device=device).manual_seed(int(bits * 10))
+    ce, cc = TurboQuantKVCache(bits=bits), TurboQuantKVCache(bits=bits)
+    compiled = torch.compile(layer, backend="aot_eager")
+    for L in (40, 1, 1, 3, 300):
+        q = torch.randn(1, 8, L, 128, device=device, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, 2, L, 128, device=device, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, 2, L, 128, device=device, generator=g).to(torch.bfloat16)
+        want = layer(ce, q, k, v)
+        got = compiled(cc, q, k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"L={L}: compiled layer differs from eager"
+        assert cc.offset == ce.offset
