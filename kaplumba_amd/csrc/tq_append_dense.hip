@@ -253,8 +253,23 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
         for (int e = 0; e < 32; ++e) {
           const float y = acc[2 * p + e / 16][e % 16];
           uint32_t idx = 0;
+          if constexpr (NMID >= 7) {
+            // thr is sorted, so the middle threshold decides which half
+            // can still hold y: count that half (H compares, its thresholds
+            // chosen by H selects) on top of the H + 1 below it or none.
+            // The same count as NMID compares, in 2H + 2 fewer operations.
+            constexpr int H = NMID / 2;
+            const bool up = GE ? (y >= thr[H]) : (y > thr[H]);
+            idx = up ? static_cast<uint32_t>(H + 1) : 0u;
 #pragma unroll
-          for (int m = 0; m < NMID; ++m) idx += (GE ? (y >= thr[m]) : (y > thr[m])) ? 1u : 0u;
+            for (int m = 0; m < H; ++m) {
+              const float t = up ? thr[H + 1 + m] : thr[m];
+              idx += (GE ? (y >= t) : (y > t)) ? 1u : 0u;
+            }
+          } else {
+#pragma unroll
+            for (int m = 0; m < NMID; ++m) idx += (GE ? (y >= thr[m]) : (y > thr[m])) ? 1u : 0u;
+          }
           const int pos = e * BITS;
           const int wi = pos >> 5;
           const int sh = pos & 31;
