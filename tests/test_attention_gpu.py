@@ -374,6 +374,8 @@ def test_plain_layers(device, kvdt, d, Hq, Hkv, L, T, lengths):
     (4, 1, 64, 1, 4, "hadamard", [1500, 1500], [0, 700], "bf16", "float32"),  # left padding
     (8, 2, 32, 4, 4, "hadamard", [33, 2000], None, "f32", "float32"),    # 128 rows, a 33-token sequence
     (2, 1, 80, 3, 3, "hadamard", None, None, "bf16", "float16"),         # L > T - causal rows see nothing
+    (8, 2, 32, 3, 2, "hadamard", [0, 1, 2600], None, "bf16", "float32"), # empty and 1-token sequences
+    (8, 2, 16, 2, 2, "dense", [700, 0], [300, 0], "f16", "float32"),     # left padding + an empty row
 ])
 def test_tile_rows(device, Hq, Hkv, L, kb, vb, rot, lengths, starts, qdt, norm):
     """64 or more query rows per kv head at d = 128: the tile kernel (K/V decoded
