@@ -20,39 +20,44 @@
 
 namespace tq {
 
-// Load 32 consecutive elements of dtype DT starting at p (16-byte aligned).
+// 32 consecutive input elements as loaded (16-byte pieces), converted to f32
+// by widen32 once they are needed.
 template <int DT>
-__device__ __forceinline__ void load32(const void* p, float (&v)[32]) {
-  if constexpr (DT == TQ_DTYPE_F32) {
-    const float4* q = static_cast<const float4*>(p);
+struct Raw32 {
+  static constexpr int N = DT == TQ_DTYPE_F32 ? 8 : 4;
+  uint4 w[N];
+};
+
+template <int DT>
+__device__ __forceinline__ void load_raw32(const void* p, Raw32<DT>& r) {
+  const uint4* q = static_cast<const uint4*>(p);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float4 t = q[i];
-      v[4 * i + 0] = t.x;
-      v[4 * i + 1] = t.y;
-      v[4 * i + 2] = t.z;
-      v[4 * i + 3] = t.w;
-    }
-  } else {
-    const uint4* q = static_cast<const uint4*>(p);
+  for (int i = 0; i < Raw32<DT>::N; ++i) r.w[i] = q[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void widen32(const Raw32<DT>& r, float (&v)[32]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint4 t = q[i];
-      uint32_t w[4] = {t.x, t.y, t.z, t.w};
+  for (int i = 0; i < Raw32<DT>::N; ++i) {
+    const uint32_t w[4] = {r.w[i].x, r.w[i].y, r.w[i].z, r.w[i].w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == TQ_DTYPE_F32) {
+        v[4 * i + j] = __uint_as_float(w[j]);
+      } else {
         const uint16_t lo = static_cast<uint16_t>(w[j] & 0xffffu);
         const uint16_t hi = static_cast<uint16_t>(w[j] >> 16);
-        if constexpr (DT == TQ_DTYPE_F16) {
-          v[8 * i + 2 * j] = f16_bits_to_f32(lo);
-          v[8 * i + 2 * j + 1] = f16_bits_to_f32(hi);
-        } else {
-          v[8 * i + 2 * j] = bf16_bits_to_f32(lo);
-          v[8 * i + 2 * j + 1] = bf16_bits_to_f32(hi);
-        }
+        v[8 * i + 2 * j] = DT == TQ_DTYPE_F16 ? f16_bits_to_f32(lo) : bf16_bits_to_f32(lo);
+        v[8 * i + 2 * j + 1] = DT == TQ_DTYPE_F16 ? f16_bits_to_f32(hi) : bf16_bits_to_f32(hi);
       }
     }
   }
+}
+
+// Workgroup barrier over LDS only: outstanding global loads stay in flight
+// across it (__syncthreads would wait for them too).
+__device__ __forceinline__ void append_lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // One block's share of a quantize launch: vectors [block * VPB, block * VPB + VPB)
@@ -64,39 +69,60 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   constexpr int NMID = (1 << BITS) - 1;
   constexpr int PW = D * BITS / 32;
   constexpr bool LUT = NMID > 3;  // bucket table beyond three midpoints
+  constexpr int SPT = (D + 255) / 256;  // sign entries per thread
   __shared__ float s_sign[D];
   __shared__ float s_mid[NMID];
   __shared__ uint2 s_qb[LUT ? kQbN : 1];
   __shared__ int s_qb_bad;
-  for (int i = threadIdx.x; i < D; i += blockDim.x) s_sign[i] = a.rot[i];
-  if (threadIdx.x < NMID) s_mid[threadIdx.x] = a.mid[threadIdx.x];
+
+  // The block's small constants are requested first, then this lane's 32
+  // input elements; the table set-up below runs while the rows are in flight.
+  float sgn[SPT];
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    sgn[k] = i < D ? a.rot[i] : 0.f;
+  }
+  const float mid_t = threadIdx.x < NMID ? a.mid[threadIdx.x] : 0.f;
+
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  const int64_t vec = block * VPB + threadIdx.x / NL;
+  const int g = threadIdx.x % NL;
+  const bool live = vec < n_vec;
+  // lanes past the last vector load vector 0 (launches have n_vec >= 1) and
+  // drop it: unconditional loads keep the wait counts exact
+  const int64_t vl = live ? vec : 0;
+  const int l = static_cast<int>(vl % a.L);
+  const int64_t bh = vl / a.L;
+  const int h = static_cast<int>(bh % a.H);
+  const int b = static_cast<int>(bh / a.H);
+  constexpr int ES = XDT == TQ_DTYPE_F32 ? 4 : 2;
+  Raw32<XDT> raw;
+  load_raw32<XDT>(static_cast<const char*>(a.x) + (b * a.sb + h * a.sh + l * a.sl + g * 32) * ES, raw);
+
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < D) s_sign[i] = sgn[k];
+  }
+  if (threadIdx.x < NMID) s_mid[threadIdx.x] = mid_t;
   if (threadIdx.x == 0) s_qb_bad = 0;
-  __syncthreads();
+  append_lds_barrier();
   if constexpr (LUT) {
     for (int t = threadIdx.x; t < kQbN; t += blockDim.x) {
       uint2 ent;
       if (!qb_entry(t, s_mid, NMID, ent)) s_qb_bad = 1;
       s_qb[t] = ent;
     }
-    __syncthreads();
+    append_lds_barrier();
   }
   const bool use_lut = LUT && s_qb_bad == 0;
 
-  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
-  const int64_t vec = block * VPB + threadIdx.x / NL;
-  const int g = threadIdx.x % NL;
   // Every lane of a vector shares `vec`, so a vector's lanes leave together
   // and the xor-shuffles below stay inside live lane groups.
-  if (vec >= n_vec) return;
-  const int l = static_cast<int>(vec % a.L);
-  const int64_t bh = vec / a.L;
-  const int h = static_cast<int>(bh % a.H);
-  const int b = static_cast<int>(bh / a.H);
-
-  const int64_t xoff = b * a.sb + h * a.sh + l * a.sl + g * 32;
-  constexpr int ES = XDT == TQ_DTYPE_F32 ? 4 : 2;
+  if (!live) return;
   float v[32];
-  load32<XDT>(static_cast<const char*>(a.x) + xoff * ES, v);
+  widen32<XDT>(raw, v);
 
   // ---- norm: in-lane fold 16, 8, 4, 2, 1 then cross-lane xor butterfly
   float s[16];
