@@ -121,34 +121,34 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
   const int64_t tile_stride = nblk / S::NSLICE;
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
 
-  // Input run of this lane for a given tile (zeros past the last vector).
+  // Input run of this lane for a given tile.  A lane past the last vector
+  // reads vector 0 (launches have n_vec >= 1) and gets row -1: its column
+  // of the products is its own and is never stored.  Loads without a branch
+  // keep the compiler's wait counts exact.
   auto load_x = [&](int64_t tile, u32x4_t (&xr)[NX], int64_t& row) {
     const int64_t vec = tile * S::VPT + wave * 32 + vl;
-    row = -1;
-    if (vec < n_vec) {
-      const int l = static_cast<int>(vec % a.L);
-      const int64_t bh = vec / a.L;
-      const int h = static_cast<int>(bh % a.H);
-      const int b = static_cast<int>(bh / a.H);
-      const int64_t xoff = b * a.sb + h * a.sh + l * a.sl + g * S::LE;
-      const u32x4_t* src =
-          reinterpret_cast<const u32x4_t*>(static_cast<const char*>(a.x) + xoff * XP::ES);
+    const int64_t vc = vec < n_vec ? vec : 0;
+    const int l = static_cast<int>(vc % a.L);
+    const int64_t bh = vc / a.L;
+    const int h = static_cast<int>(bh % a.H);
+    const int b = static_cast<int>(bh / a.H);
+    const int64_t xoff = b * a.sb + h * a.sh + l * a.sl + g * S::LE;
+    const u32x4_t* src =
+        reinterpret_cast<const u32x4_t*>(static_cast<const char*>(a.x) + xoff * XP::ES);
 #pragma unroll
-      for (int i = 0; i < NX; ++i) xr[i] = src[i];
-      row = (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l;
-    } else {
-#pragma unroll
-      for (int i = 0; i < NX; ++i) xr[i] = u32x4_t{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < NX; ++i) xr[i] = src[i];
+    row = vec < n_vec ? (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l : -1;
   };
 
-  int64_t tile = bid / S::NSLICE;
-  u32x4_t xr[NX];
-  int64_t row;
-  load_x(tile, xr, row);  // in flight while R is split into LDS
-
-  // ---- R pieces -> LDS in A-fragment order
-  for (int f = tid; f < S::NT * S::KS * kWave; f += kDenseThreads) {
+  // ---- R pieces -> LDS in A-fragment order.  This thread's fragments are
+  // requested first, then its first input tile, so the tile's loads are in
+  // flight while R is split (waiting for R does not wait for them).
+  constexpr int FPT = S::NT * S::KS * kWave / kDenseThreads;  // fragments per thread
+  static_assert(S::NT * S::KS * kWave % kDenseThreads == 0, "R fragments per thread");
+  float4 rv[FPT][2];
+#pragma unroll
+  for (int i = 0; i < FPT; ++i) {
+    const int f = tid + i * kDenseThreads;
     const int ln = f % kWave;
     const int ks = (f / kWave) % S::KS;
     const int t = f / (kWave * S::KS);
@@ -156,7 +156,17 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
     const int coord = c0 + 64 * (t / 2) + 32 * ((r >> 2) & 1) + 16 * (t & 1) + 4 * (r >> 3) + (r & 3);
     const float4* src =
         reinterpret_cast<const float4*>(a.rot + static_cast<int64_t>(coord) * D + (ln / 32) * S::LE + 8 * ks);
-    const float4 v0 = src[0], v1 = src[1];
+    rv[i][0] = src[0];
+    rv[i][1] = src[1];
+  }
+  int64_t tile = bid / S::NSLICE;
+  u32x4_t xr[NX];
+  int64_t row;
+  load_x(tile, xr, row);
+#pragma unroll
+  for (int i = 0; i < FPT; ++i) {
+    const int f = tid + i * kDenseThreads;
+    const float4 v0 = rv[i][0], v1 = rv[i][1];
     const float e[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     uint32_t w[S::NRP][4];
 #pragma unroll
