@@ -363,13 +363,18 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   // A trailing word past its span may belong to the next token's row or lie
   // past t_end (buffer range checks are per dword: it reads zero); its bits
   // are never used.
-  auto load_sub = [&](Buf& bf, int s0) {
+  // The key words feed scores(), the norms and value words finish(); the
+  // two halves of a buffer are refilled separately (see the loop).
+  auto load_keys = [&](Buf& bf, int s0) {
+    const uint32_t ko = static_cast<uint32_t>(s0) * (PWK * 4) + k_lane;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) load_words<KRAW>(bf.k[tt], krs, ko + tt * 16 * PWK * 4);
+  };
+  auto load_rest = [&](Buf& bf, int s0) {
     const uint32_t t0 = static_cast<uint32_t>(s0);
-    const uint32_t ko = t0 * (PWK * 4) + k_lane;
     const uint32_t no = t0 * nb + n_lane;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      load_words<KRAW>(bf.k[tt], krs, ko + tt * 16 * PWK * 4);
       bf.nk[tt] = load_norm_raw(knrs, no + tt * 16 * nb);
       bf.nv[tt] = load_norm_raw(vnrs, no + tt * 16 * nb);
     }
@@ -379,6 +384,10 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
 #pragma unroll
       for (int k = 0; k < NSEG; ++k)
         load_words<VRAW>(bf.v[e][k], vrs, vo + v_lane[k] + e * PWV * 4);
+  };
+  auto load_sub = [&](Buf& bf, int s0) {
+    load_keys(bf, s0);
+    load_rest(bf, s0);
   };
 
   // ---- prologue loads first (the query elements of this wave's rows, key
@@ -736,8 +745,13 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   // Prefetches are issued unconditionally (past the end they are free), so
   // the compiler's count of outstanding loads is exact and each sub-chunk
   // waits for its own loads only.
+  // Buffer s % P holds sub-chunk s.  A buffer's key words are refilled as
+  // soon as scores() has read them (sub-chunk i + 1 + P right after the
+  // scores of i + 1), its norms and value words after finish(): the key
+  // loads are in flight for about two steps, not only during one finish().
   f32x4_t Sc[2];
   if (n_my > 0) scores(buf[0], Sc);
+  load_keys(buf[0], sub_start(P));
   for (int base = 0; base < n_my; base += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
@@ -746,7 +760,8 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
         finish(buf[s], Sc, sub_start(i));
         if (i + 1 < n_my) scores(buf[(s + 1) % P], Sc);
       }
-      load_sub(buf[s], sub_start(i + P));
+      load_rest(buf[s], sub_start(i + P));
+      load_keys(buf[(s + 1) % P], sub_start(i + 1 + P));
     }
   }
 
