@@ -20,8 +20,8 @@ import torch
 
 from . import _lib
 from . import codebook as cbmod
-from .ops import (Codec, _attention_general, _capacity_of, _require_device, _seq_array, _stream,
-                  _workspace)
+from .ops import (Codec, _attention_general, _capacity_of, _fields, _opt_tensor, _require_device,
+                  _seq_array, _stream, _workspace)
 
 __all__ = ["ProdCodec", "TurboQuantProdState", "attention_prod"]
 
@@ -74,8 +74,11 @@ class ProdCodec:
             torch.zeros((B, H, cap), dtype=norm_dtype, device=device),
             torch.zeros((B, H, cap, self.sign_width), dtype=torch.uint32, device=device))
 
-    def quantize_into(self, x: torch.Tensor, st: TurboQuantProdState, offset: int) -> None:
+    def quantize_into(self, x: torch.Tensor, st: TurboQuantProdState, offset: int,
+                      _direct: bool = False) -> None:
         """Quantize x (B, H, L, D) into rows offset .. offset + L of capacity buffers."""
+        if not _direct and torch.compiler.is_compiling():
+            return torch.ops.kaplumba.prod_quantize(x, *st, offset, self.dim, self.bits, self.seed)
         _require_device(x, *st)
         B, H, L, D = x.shape
         if D != self.dim:
@@ -111,8 +114,10 @@ class ProdCodec:
         self.quantize_into(vectors, st, 0)
         return st
 
-    def dequantize(self, state: TurboQuantProdState) -> torch.Tensor:
+    def dequantize(self, state: TurboQuantProdState, _direct: bool = False) -> torch.Tensor:
         """``dequantize`` (:4668-4677): f32 (B, H, T, D)."""
+        if not _direct and torch.compiler.is_compiling():
+            return torch.ops.kaplumba.prod_dequantize(*state, self.dim, self.bits, self.seed)
         _require_device(*state)
         B, H, T = state.norms.shape
         cap = _capacity_of(state.norms, state.qjl_signs, self.sign_width)
@@ -134,13 +139,19 @@ class ProdCodec:
 def attention_prod(queries: torch.Tensor, keys: TurboQuantProdState, v_norms: torch.Tensor,
                    v_idx: torch.Tensor, key_codec: ProdCodec, value_codec: Codec, scale: float,
                    causal: bool, seq_lens: Optional[torch.Tensor] = None,
-                   seq_starts: Optional[torch.Tensor] = None, mask=None) -> torch.Tensor:
+                   seq_starts: Optional[torch.Tensor] = None, mask=None,
+                   _direct: bool = False) -> torch.Tensor:
     """Attention with Prod-coded keys and MSE-coded values (``tq_attention_prod``):
     the fused Prod decode kernel's scores (turboquant_cache.py:2000-2206) with
     ``quantized_attention``'s softmax and masks.  Views (B, Hkv, T[, W]) of
     contiguous capacity buffers, as the cache hands them out.  ``mask`` is an
     optional array mask (``ops.prepare_mask``); a value codec of another dim or
     rotation, or a mask, runs ``tq_attention_general``."""
+    if not _direct and torch.compiler.is_compiling():
+        return torch.ops.kaplumba.attention_prod(
+            queries, *keys, v_norms, v_idx, key_codec.dim, key_codec.bits, key_codec.seed,
+            *_fields(value_codec), float(scale), bool(causal), _opt_tensor(seq_lens, torch.int32),
+            _opt_tensor(seq_starts, torch.int32), _opt_tensor(mask, None))
     _require_device(queries, *keys, v_norms, v_idx)
     B, Hq, L, D = queries.shape
     Hkv, T = keys.norms.shape[1], keys.norms.shape[2]

@@ -11,7 +11,7 @@ from torch.fx.experimental.proxy_tensor import make_fx
 from kaplumba_amd import ops
 
 OPS = ("append_quantize", "append_quantize_kv", "append_plain", "dequantize", "attention_packed",
-       "attention_plain")
+       "attention_plain", "prod_quantize", "prod_dequantize", "attention_prod")
 
 
 def _schema(name):
@@ -26,6 +26,9 @@ def test_operators_registered_with_mutations_declared():
         "dequantize": set(),
         "attention_packed": set(),
         "attention_plain": set(),
+        "prod_quantize": {"norms", "mse_indices", "residual_norms", "qjl_signs"},
+        "prod_dequantize": set(),
+        "attention_prod": set(),
     }
     for name in OPS:
         s = _schema(name)
@@ -54,6 +57,12 @@ def test_fake_shapes():
         q16 = q.to(torch.float16)
         o = torch.ops.kaplumba.attention_plain(q16, keys, vals, 0.1, False, None, None, None)
         assert (o.shape, o.dtype) == ((B, Hq, L, 96), torch.float16)
+        sg = torch.empty(B, Hkv, cap, 4, device="cuda", dtype=torch.uint32)[:, :, :T]
+        o = torch.ops.kaplumba.attention_prod(q, kn, kp, kn, sg, kn, vp, 128, 3, 0, *f(vc), 0.1,
+                                              True, None, None, None)
+        assert (o.shape, o.dtype) == ((B, Hq, L, 64), torch.bfloat16)
+        dq = torch.ops.kaplumba.prod_dequantize(kn, kp, kn, sg, 128, 3, 0)
+        assert (dq.shape, dq.dtype) == ((B, Hkv, T, 128), torch.float32)
 
 
 def test_step_traces_into_one_graph():

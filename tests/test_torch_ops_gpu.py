@@ -117,8 +117,8 @@ def test_opcheck_every_operator(device):
                           (q, plain[:, :, :T], plain[:, :, :T], 0.125, False, None, None, mask))
 
 
-@pytest.mark.parametrize("bits", [3, 3.5])
-def test_compiled_cache_layer_matches_eager(device, bits):
+@pytest.mark.parametrize("bits,quantizer", [(3, "mse"), (3.5, "mse"), (3, "prod")])
+def test_compiled_cache_layer_matches_eager(device, bits, quantizer):
     """A model layer's cache calls (update_and_fetch, then the SDPA dispatch) under
     torch.compile: prefill, cache growth and decode steps give the eager bits."""
     from kaplumba_amd import TurboQuantKVCache, scaled_dot_product_attention
@@ -131,7 +131,8 @@ def test_compiled_cache_layer_matches_eager(device, bits):
         return scaled_dot_product_attention(q, ks, vs, cache, 1 / math.sqrt(q.shape[-1]), mask)
 
     g = torch.Generator(device=device).manual_seed(int(bits * 10))
-    ce, cc = TurboQuantKVCache(bits=bits), TurboQuantKVCache(bits=bits)
+    ce = TurboQuantKVCache(bits=bits, key_quantizer=quantizer)
+    cc = TurboQuantKVCache(bits=bits, key_quantizer=quantizer)
     compiled = torch.compile(layer, backend="aot_eager")
     for L in (40, 1, 1, 3, 300):
         q = torch.randn(1, 8, L, 128, device=device, generator=g).to(torch.bfloat16)
@@ -142,3 +143,24 @@ def test_compiled_cache_layer_matches_eager(device, bits):
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"L={L}: compiled layer differs from eager"
         assert cc.offset == ce.offset
+
+
+def test_opcheck_prod_operators(device):
+    from kaplumba_amd import prod
+
+    g = torch.Generator(device=device).manual_seed(13)
+    B, Hq, Hkv, cap, T, d = 1, 4, 2, 96, 70, 128
+    pc, vc = prod.ProdCodec(d, 3, 0), ops.Codec(d, 3, 1)
+    x = torch.randn(B, Hkv, T, d, device=device, generator=g).to(torch.bfloat16)
+    st = pc.alloc(B, Hkv, cap, device)
+    torch.library.opcheck(torch.ops.kaplumba.prod_quantize.default, (x, *st, 0, d, 3, 0))
+    pc.quantize_into(x, st, 0)
+    view = [t[:, :, :T] for t in st]
+    torch.library.opcheck(torch.ops.kaplumba.prod_dequantize.default, (*view, d, 3, 0))
+    vp = torch.zeros(B, Hkv, cap, vc.packed_width, dtype=torch.uint32, device=device)
+    vn = torch.zeros(B, Hkv, cap, dtype=torch.float32, device=device)
+    ops.append_quantize(x, vc, vp, vn, 0)
+    q = torch.randn(B, Hq, 1, d, device=device, generator=g).to(torch.bfloat16)
+    torch.library.opcheck(torch.ops.kaplumba.attention_prod.default,
+                          (q, *view, vn[:, :, :T], vp[:, :, :T], d, 3, 0, *ops._fields(vc), 0.09,
+                           False, None, None, None))
