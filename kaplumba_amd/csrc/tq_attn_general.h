@@ -93,6 +93,7 @@ struct GenParams {
   float qjl_scale;           // f32(sqrt(pi/2) / Dk)
   int po_natural;            // partials already in the natural value basis (plain values)
   int merge_had;             // the element-wise merge applies R_V^-1 (Hadamard) per merged row
+  int merge_bpp;             // > 0: flat-merge blocks per (b, kv head), mapped to that pair's XCD
   uint32_t* qhl;             // tile kernel: per query row, q_rot * sq as hi then lo f16 [rows, 2, Dk / 2] u32
   float* qsq;                // tile kernel: sq per query row
   void* out;                 // [B, Hq, L, Dv] in the query dtype

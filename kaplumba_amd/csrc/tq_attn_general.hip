@@ -593,7 +593,15 @@ __global__ __launch_bounds__(kGenThreads) void gen_merge_kernel(GenParams p) {
 // fits, so no 64-bit divisions.
 template <typename I>
 __global__ __launch_bounds__(256) void gen_merge_flat_kernel(GenParams p, I n_items) {
-  const I idx = static_cast<I>(blockIdx.x) * 256 + static_cast<I>(threadIdx.x);
+  I blk = static_cast<I>(blockIdx.x);
+  if (p.merge_bpp > 0) {
+    // the blocks of (b, kv head) pair q run on XCD q % 8, where the tile
+    // kernel wrote that pair's partials (workgroup id % 8 picks the XCD)
+    const I k = blk >> 3;
+    const I pair = (blk & 7) + 8 * (k / p.merge_bpp);
+    blk = pair * p.merge_bpp + k % p.merge_bpp;
+  }
+  const I idx = blk * 256 + static_cast<I>(threadIdx.x);
   if (idx >= n_items) return;
   const int C4 = p.Dv / 4;
   const I RL = static_cast<I>(p.R) * p.L;
@@ -1025,6 +1033,12 @@ int general_attention(const GenCall& c) {
   if (rc) return rc;
   if (plain || p.merge_had) {
     const int64_t items = static_cast<int64_t>(c.B) * c.Hkv * (c.Hq / c.Hkv) * c.L * (c.Dv / 4);
+    const int64_t pair_items = static_cast<int64_t>(c.Hq / c.Hkv) * c.L * (c.Dv / 4);
+    // after the tile kernel, each pair's merge blocks run on the XCD whose
+    // L2 took that pair's partials
+    p.merge_bpp = (tile && (static_cast<int64_t>(c.B) * c.Hkv) % 8 == 0 && pair_items % 256 == 0)
+                      ? static_cast<int>(pair_items / 256)
+                      : 0;
     const dim3 fgrid(static_cast<unsigned>((items + 255) / 256));
     if (items < (int64_t(1) << 31) - 256)
       hipLaunchKernelGGL(gen_merge_flat_kernel<int>, fgrid, dim3(256), 0, st, p, static_cast<int>(items));
