@@ -48,6 +48,10 @@ CFG4 = dict(B=4, Hq=32, Hkv=8, L=4, T=131072 + 4, D=128, kb=2, vb=1)
 # prefill attention: one prefill_step_size chunk (256 queries) at the end of an
 # 8192-token prompt, config-1 heads and widths, causal
 CFGP = dict(B=1, Hq=32, Hkv=8, L=256, T=8192, D=128, bits=3)
+CODEBOOK_NOTE = ("every leg uses the Beta Lloyd-Max codebooks the reference cache builds "
+                 "(turboquant_cache.py:3587-3642); BASELINE's configs 0, 1 and 4 name the N(0,1) "
+                 "Lloyd-Max codebook, which the kernels take as data at the same speed and which the "
+                 "full-size GPU tests run against the oracle")
 
 
 def algorithmic_decode_bytes(Hkv, T, D, kb, vb, norm_bytes, B=1):
@@ -141,6 +145,69 @@ def bench_decode(torch, args, dev):
                 rotate_mb=n_layers * per_layer / 1e6, cpu_sample=sample)
 
 
+def bench_floor(torch, dev, per_call, n_bufs):
+    """The HBM floor the headline is read against, measured with the probe
+    kernels of kaplumba_amd/libkaplumba_probe.so (roofline_probe.hip):
+
+    * stream read: one launch reads `per_call` bytes (the cfg1 call's
+      algorithmic bytes) with 16-byte nontemporal loads and writes nothing;
+      launches walk `n_bufs` distinct buffers in a HIP graph, as the attention
+      calls walk distinct layer caches; best of a small sweep of grid sizes
+      and loads in flight.
+    * device copy: 1 GiB copied (read + write counted), best of three grids.
+    """
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "kaplumba_amd", "libkaplumba_probe.so"))
+    lib.tqp_stream_read.restype = ctypes.c_int
+    lib.tqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p]
+    lib.tqp_copy.restype = ctypes.c_int
+    lib.tqp_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    bufs = [torch.empty(per_call, dtype=torch.uint8, device=dev) for _ in range(n_bufs)]
+    for b in bufs:
+        b.fill_(1)
+    sink = torch.zeros(1 << 16, dtype=torch.uint32, device=dev)
+    best = None
+    for blocks in (256, 512, 1024, 2048):
+        for unroll in (4, 8):
+            def step(i, blocks=blocks, unroll=unroll):
+                rc = lib.tqp_stream_read(bufs[i % n_bufs].data_ptr(), per_call, sink.data_ptr(), blocks,
+                                         unroll, torch.cuda.current_stream(dev).cuda_stream)
+                if rc:
+                    raise RuntimeError(f"tqp_stream_read: HIP error {rc}")
+            ms, _, _ = graph_timed(torch, step, 4 * n_bufs, 4, dev)
+            if best is None or ms < best[0]:
+                best = (ms, blocks, unroll)
+    del bufs
+    _free(torch)
+    nbytes = 1 << 30
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    best_c = None
+    for blocks in (1024, 4096, 16384):
+        def cstep(_i, blocks=blocks):
+            rc = lib.tqp_copy(src.data_ptr(), dst.data_ptr(), nbytes, blocks,
+                              torch.cuda.current_stream(dev).cuda_stream)
+            if rc:
+                raise RuntimeError(f"tqp_copy: HIP error {rc}")
+        ms, _, _ = graph_timed(torch, cstep, 5, 1, dev)
+        if best_c is None or ms < best_c[0]:
+            best_c = (ms, blocks)
+    if not torch.equal(dst[:: 1 << 20], src[:: 1 << 20]):
+        raise RuntimeError("tqp_copy: copy differs from its source")
+    del src, dst
+    _free(torch)
+    ms, blocks, unroll = best
+    return {"stream_read": {"bytes_per_launch": per_call, "us_per_launch": round(ms * 1e3, 3),
+                            "GB/s": round(per_call / (ms * 1e-3) / 1e9, 2),
+                            "launch": f"{blocks} x 256 threads, {unroll} 16-byte loads in flight per "
+                                      f"thread, {n_bufs} distinct buffers in a HIP graph"},
+            "device_copy": {"bytes": nbytes, "GB/s": round(2 * nbytes / (best_c[0] * 1e-3) / 1e9, 2),
+                            "us": round(best_c[0] * 1e3, 2), "launch": f"{best_c[1]} x 256 threads",
+                            "note": "read + write bytes"}}
+
+
 def bench_quantize(torch, args, dev):
     """Config 0: append-quantize K and V f16 [1, 8, 4096, 128] at 3 bits (one layer)."""
     from kaplumba_amd import ops
@@ -225,7 +292,7 @@ def bench_ragged(torch, args, dev):
     _free(torch)
     gbs = per_step / (ms * 1e-3) / 1e9
     return {"workload": "cfg2 ragged decode: 32 seqs, T~U[2048,8192] (seed 1004), 16 q / 8 kv heads, "
-                        "d=256, K 4-bit / V 2-bit, dense 256x256 rotation, f32 norms",
+                        "d=256, K 4-bit / V 2-bit, dense 256x256 rotation, f32 norms, Beta codebooks",
             "value": round(gbs, 2), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "us_per_step": round(ms * 1e3, 3), "sum_tokens": int(lens.sum()),
             "bytes_per_step": per_step, "decode_tokens_per_s": round(c["B"] * 1e3 / ms, 1),
@@ -285,7 +352,8 @@ def bench_prefill_append(torch, args, dev):
     launch_us = ms_q * 1e3 / (2 * n_q)                      # per K or V tensor (half a K+V launch)
     flops = 2.0 * H * T * D * D                             # u @ R^T per tensor
     return {"workload": "cfg3 prefill append: 36 layers x bf16 K,V [8,8192,128]; layers 0-3 stored "
-                        "unquantized, 4-35 dense 128x128 rotation (matrix cores) + 3-bit pack, f32 norms",
+                        "unquantized, 4-35 dense 128x128 rotation (matrix cores) + 3-bit pack, f32 norms, "
+                        "Beta codebook",
             "value": round(total / (ms * 1e-3) / 1e9, 2), "unit": "GB/s",
             "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "us_per_step": round(ms * 1e3, 2), "bytes_per_step": total,
@@ -350,7 +418,7 @@ def bench_verify(torch, args, dev):
     gbs = per_step / (ms * 1e-3) / 1e9
     gbs_p = plain_bytes / (ms_p * 1e-3) / 1e9
     return {"workload": "cfg4 verify: batch 4 x 4 causal drafts, 32 q / 8 kv heads, d=128, "
-                        "131076 tokens, K 2-bit / V 1-bit, Hadamard rotation, f32 norms",
+                        "131076 tokens, K 2-bit / V 1-bit, Hadamard rotation, f32 norms, Beta codebooks",
             "value": round(gbs, 2), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "us_per_step": round(ms * 1e3, 3), "bytes_per_step": per_step,
             "verified_tokens_per_s": round(B * c["L"] * 1e3 / ms, 1), "steps": steps,
@@ -391,7 +459,8 @@ def bench_prefill_attention(torch, args, dev):
     flops = 4.0 * B * Hq * D * visible
     tflops = flops / (ms * 1e-3) / 1e12
     return {"workload": "prefill attention: one 256-query causal chunk ending an 8192-token "
-                        "prompt, 32 q / 8 kv heads, d=128, 3-bit K/V, Hadamard rotation, f32 norms",
+                        "prompt, 32 q / 8 kv heads, d=128, 3-bit K/V, Hadamard rotation, f32 norms, "
+                        "Beta codebook",
             "value": round(tflops, 2), "unit": "TFLOP/s",
             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
             "roofline": "mfma (f16/bf16 dense peak 2500 TFLOP/s)",
@@ -439,7 +508,7 @@ def bench_prod_decode(torch, args, dev):
     gbs = per_step / (ms * 1e-3) / 1e9
     return {"workload": "cfg1 decode with Prod keys: 3-bit Prod K (2-bit MSE + 1-bit QJL signs, "
                         "f32 norm and residual norm) and 3-bit MSE V, 32 q / 8 kv heads, d=128, "
-                        "32768 tokens",
+                        "32768 tokens, Beta codebooks",
             "value": round(gbs, 2), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "us_per_step": round(ms * 1e3, 3), "bytes_per_step": per_step,
             "note": "one call = qprep_kernel (q @ P^T) + attn_small_kernel (Prod) + attn_merge_kernel",
@@ -528,6 +597,7 @@ def main():
     dev = torch.device("cuda", 0)
     dec = bench_decode(torch, args, dev)
     _free(torch)
+    floor = bench_floor(torch, dev, dec["bytes"], dec["n_layers"])
     legs = {x.strip() for x in args.legs.split(",") if x.strip()}
     unknown = legs - {"cfg0", "cfg2", "cfg3", "cfg4", "prefill", "prod"}
     if unknown:
@@ -547,7 +617,9 @@ def main():
         "dtype": "f32 (3-bit packed K/V, bf16 q/out)",
         "data": "synthetic",
         "config": {"workload": "cfg1 decode attention, 3-bit TurboQuant KV, batch 1, 32 q heads / "
-                               "8 kv heads, d=128, 32768 tokens, Hadamard rotation, f32 norms",
+                               "8 kv heads, d=128, 32768 tokens, Hadamard rotation, f32 norms, "
+                               "Beta Lloyd-Max codebook (the reference's live _codebook)",
+                   "codebook_note": CODEBOOK_NOTE,
                    "tokens": args.tokens, "bytes_per_step": dec["bytes"],
                    "distinct_layer_caches": dec["n_layers"], "rotated_mb": round(dec["rotate_mb"], 1),
                    "decode_tokens_per_s": round(1e3 / dec["ms_per_step"], 1),
@@ -557,6 +629,13 @@ def main():
                      "traffic": CFG1_TRAFFIC_BYTES,
                      "traffic_note": "HBM bytes per call from rocprofv3 FETCH_SIZE/WRITE_SIZE, "
                                      "copy-calibrated; algorithmic bytes are 27,262,976",
+                     "frac_of_copy_peak": round(value / floor["stream_read"]["GB/s"], 4),
+                     "frac_of_device_copy": round(value / floor["device_copy"]["GB/s"], 4),
+                     "copy_peak": floor,
+                     "copy_peak_note": "frac_of_copy_peak = achieved / the stream-read probe moving "
+                                       "the same bytes per launch over the same number of distinct "
+                                       "buffers (the floor of one call); frac_of_device_copy = "
+                                       "achieved / a 1 GiB device copy",
                      "kernel": "attention call: attn_stage_kernel<128,3,3> + attn_merge_rot_kernel<128>",
                      "call_us": round(dec["ms_per_step"] * 1e3, 3),
                      "achieved_note": "algorithmic bytes / time of one whole attention call (both "
@@ -568,7 +647,7 @@ def main():
         _free(torch)
         line["quantize"] = {"workload": "cfg0 append-quantize K+V f16 [1,8,4096,128] 3-bit (one "
                                         "tq_append_quantize_kv call, as update_and_fetch makes), "
-                                        "Hadamard rotation",
+                                        "Hadamard rotation, Beta codebook",
                             "value": round(qnt["bytes"] / (qnt["ms_per_step"] * 1e-3) / 1e9, 2),
                             "unit": "GB/s", "step_us": round(qnt["ms_per_step"] * 1e3, 3)}
     if "cfg2" in legs:

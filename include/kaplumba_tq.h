@@ -160,12 +160,16 @@ int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed, const void
                        const float* projection, float* out, void* stream);
 
 /*
- * Bytes of workspace tq_attention() needs for this problem (split-K partials
- * and rotated queries).  max_tokens is the largest
- * per-sequence cache length.
+ * Bytes of workspace tq_attention() / tq_attention_ranged() need for this
+ * problem (split-K partials and rotated queries).  max_tokens is the largest
+ * per-sequence cache length.  tq_attention_prod_workspace_size() is the same
+ * for tq_attention_prod (its general-kernel shapes add a projected-query
+ * region).
  */
 int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
                                     int64_t max_tokens);
+int64_t tq_attention_prod_workspace_size(int B, int Hq, int Hkv, int L, int dim,
+                                         int64_t max_tokens);
 
 /*
  * Decode / speculative-verify attention straight from the cache.
@@ -243,7 +247,8 @@ int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int 
  * is not read for k_bits == 1).  Dim 64 / 128 with at most 4 query rows per kv
  * head (Hq/Hkv * L) and k_bits >= 2 run the fused row-group kernel; every
  * other shape (power-of-two dims 32..512) runs the kernels of
- * tq_attention_general.  Workspace as tq_attention.
+ * tq_attention_general.  Workspace as tq_attention, sized by
+ * tq_attention_prod_workspace_size().
  */
 int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
                       int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,
@@ -256,20 +261,6 @@ int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L,
                       int causal, void* out, void* workspace, int64_t workspace_bytes,
                       void* stream);
 
-/*
- * tq_attention_ranged without a workspace argument, for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  No counterpart in the reference, which
- * never exposes a workspace.  The split partials and rotated queries live in
- * a static device array of TQ_NOALLOC_SCRATCH_BYTES per GPU, held until the
- * process ends; the entry point calls no hipMalloc / hipFree.  Problems whose
- * tq_attention_workspace_size() exceeds that size return TQ_ERR_WORKSPACE
- * (use tq_attention with a caller workspace).  Every call on one GPU shares
- * the array: calls that overlap on that GPU (other streams, other host
- * threads) race.  No initial contents are needed: a call writes every
- * scratch byte it reads.  Every other argument and the results are those of
- * tq_attention_ranged.
- */
 /*
  * Bytes of workspace tq_attention_general() needs (rotated and projected
  * queries, split partials).
@@ -319,6 +310,20 @@ int tq_attention_general(const void* q, int q_dtype, int B, int Hq, int Hkv, int
                          int causal, const void* mask, int mask_kind, const int64_t* mask_strides,
                          void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * tq_attention_ranged without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, which
+ * never exposes a workspace.  The split partials and rotated queries live in
+ * a static device array of TQ_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends; the entry point calls no hipMalloc / hipFree.  Problems whose
+ * tq_attention_workspace_size() exceeds that size return TQ_ERR_WORKSPACE
+ * (use tq_attention with a caller workspace).  Every call on one GPU shares
+ * the array: calls that overlap on that GPU (other streams, other host
+ * threads) race.  No initial contents are needed: a call writes every
+ * scratch byte it reads.  Every other argument and the results are those of
+ * tq_attention_ranged.
+ */
 #define TQ_NOALLOC_SCRATCH_BYTES (16ll << 20)
 int tq_attention_noalloc(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
                          int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_l, float scale,

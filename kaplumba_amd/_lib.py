@@ -63,6 +63,7 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int64,
         c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "tq_attention_workspace_size": (c_int64, [c_int, c_int, c_int, c_int, c_int, c_int64]),
+    "tq_attention_prod_workspace_size": (c_int64, [c_int, c_int, c_int, c_int, c_int, c_int64]),
     "tq_attention": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,   # q, dtype, B, Hq, Hkv, L, dim
         c_int64, c_int64, c_int64, c_float,                    # q strides, scale

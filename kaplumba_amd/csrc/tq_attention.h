@@ -93,11 +93,11 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
 
 // Packed caches whose row group is at most 4 query rows (GQA decode with
 // R <= 4, or verify with R * L <= 4) at head dim 64 / 128 run the small
-// row-group kernel (tq_attn_small.h).
+// row-group kernels: MSE-coded keys the LDS-staged kernel of tq_attn_stage.h,
+// Prod-coded keys attn_small_kernel (tq_attn_small.h).  Their launch packs
+// the kv head count into kSmallRowsHkvBits bits.
 bool small_rows_path(int kv_kind, int D, int rows);
-// Of those, MSE-coded keys run the LDS-staged kernel of tq_attn_stage.h
-// (KAPLUMBA_TQ_STAGE=0 selects attn_small_kernel instead, for comparisons).
-bool stage_path();
+constexpr int kSmallRowsHkvBits = 12;
 // Packed caches at head dim 128 with more rows run 16-row groups on the
 // register-softmax kernel of tq_attn_rows16.h.
 bool rows16_path(int kv_kind, int D, int rows);

@@ -1,7 +1,6 @@
 // Dense-rotation query preparation, split planning and the C-ABI entry of
 // attention.  The attention work itself is the fused kernel of tq_attn_impl.h.
 #include <algorithm>
-#include <cstdlib>
 #include <mutex>
 
 #include "tq_attn_general.h"
@@ -114,29 +113,11 @@ void launch_qprep(const AttnParams& p, int q_dtype, int64_t rows, hipStream_t st
 
 // ------------------------------------------------------------- planning ---
 bool small_rows_path(int kv_kind, int D, int rows) {
-  // KAPLUMBA_TQ_SMALL_ROWS=0 selects the general kernel + merge kernel instead
-  static const bool enabled = [] {
-    const char* e = getenv("KAPLUMBA_TQ_SMALL_ROWS");
-    return !(e && e[0] == '0');
-  }();
-  return enabled && kv_kind == TQ_KV_PACKED && D <= 128 && rows <= 4;
-}
-
-bool stage_path() {
-  static const bool enabled = [] {
-    const char* e = getenv("KAPLUMBA_TQ_STAGE");
-    return !(e && e[0] == '0');
-  }();
-  return enabled;
+  return kv_kind == TQ_KV_PACKED && D <= 128 && rows <= 4;
 }
 
 bool rows16_path(int kv_kind, int D, int rows) {
-  // KAPLUMBA_TQ_ROWS16=0 selects the general kernel instead
-  static const bool enabled = [] {
-    const char* e = getenv("KAPLUMBA_TQ_ROWS16");
-    return !(e && e[0] == '0');
-  }();
-  return enabled && kv_kind == TQ_KV_PACKED && D == 128 && rows > 4;
+  return kv_kind == TQ_KV_PACKED && D == 128 && rows > 4;
 }
 
 SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool packed) {
@@ -150,25 +131,15 @@ SplitPlan plan_splits(int B, int Hq, int Hkv, int L, int64_t T, int D, bool pack
   sp.nq = (rows <= 4 || D >= 256) ? 4 : 16;
   sp.n_rg = (rows + sp.nq - 1) / sp.nq;
   const int64_t base = static_cast<int64_t>(B) * Hkv * sp.n_rg;
-  // workgroups in flight per CU the split count aims for (KAPLUMBA_TQ_WG_PER_CU)
-  static const int per_cu = [] {
-    const char* e = getenv("KAPLUMBA_TQ_WG_PER_CU");
-    const int v = e ? atoi(e) : 1;
-    return v >= 1 && v <= 64 ? v : 1;
-  }();
-  const int64_t target = static_cast<int64_t>(per_cu) * device_cu_count();
+  // one workgroup in flight per CU (measured at the 32k-token decode: two or
+  // three per CU, with twice or three times the splits, ran slower)
+  const int64_t target = device_cu_count();
   int64_t ns = base > 0 ? (target + base - 1) / base : 1;
   const int64_t max_by_tokens = std::max<int64_t>(1, (T + 255) / 256);
   ns = std::max<int64_t>(1, std::min(ns, max_by_tokens));
   int64_t chunk = (T + ns - 1) / ns;
   chunk = std::max<int64_t>(256, (chunk + 255) / 256 * 256);  // whole sub-chunks for every wave
-  // longest split (KAPLUMBA_TQ_MAX_CHUNK overrides, for tuning)
-  static const int max_chunk = [] {
-    const char* e = getenv("KAPLUMBA_TQ_MAX_CHUNK");
-    const int v = e ? atoi(e) : kMaxChunk;
-    return v >= 256 && v <= (1 << 24) ? v / 256 * 256 : kMaxChunk;
-  }();
-  chunk = std::min<int64_t>(chunk, max_chunk);
+  chunk = std::min<int64_t>(chunk, kMaxChunk);
   sp.chunk = static_cast<int>(chunk);
   sp.n_splits = static_cast<int>(std::max<int64_t>(1, (T + chunk - 1) / chunk));
   return sp;
@@ -190,17 +161,31 @@ int64_t workspace_bytes(const SplitPlan& sp, int B, int Hq, int Hkv, int L, int 
 
 using namespace tq;
 
-extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
-                                               int64_t max_tokens) {
+namespace {
+
+// Workspace of one attention call: the larger of the tuned kernels' layout
+// (either cache kind) and the general kernels' (the shapes outside the tuned
+// ones); Prod keys add a projected-query region to the latter.
+int64_t attention_workspace_bytes(int B, int Hq, int Hkv, int L, int dim, int64_t max_tokens, bool prod) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || dim <= 0 || max_tokens < 0 || Hq % Hkv)
     return 0;
-  // large enough for either cache kind and for the general kernels, which
-  // serve the shapes outside the tuned ones
   const int64_t T = std::max<int64_t>(max_tokens, 1);
   const int64_t tuned =
       std::max(workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, true), B, Hq, Hkv, L, dim),
                workspace_bytes(plan_splits(B, Hq, Hkv, L, T, dim, false), B, Hq, Hkv, L, dim));
-  return std::max(tuned, general_workspace_bytes(B, Hq, Hkv, L, dim, dim, T, true));
+  return std::max(tuned, general_workspace_bytes(B, Hq, Hkv, L, dim, dim, T, prod));
+}
+
+}  // namespace
+
+extern "C" int64_t tq_attention_workspace_size(int B, int Hq, int Hkv, int L, int dim,
+                                               int64_t max_tokens) {
+  return attention_workspace_bytes(B, Hq, Hkv, L, dim, max_tokens, false);
+}
+
+extern "C" int64_t tq_attention_prod_workspace_size(int B, int Hq, int Hkv, int L, int dim,
+                                                    int64_t max_tokens) {
+  return attention_workspace_bytes(B, Hq, Hkv, L, dim, max_tokens, true);
 }
 
 namespace {
@@ -318,6 +303,10 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   if (!q || !out || !workspace) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null pointer");
   if (max_tokens > 0 && (!k || !v)) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null cache pointer");
   const int64_t T = std::max<int64_t>(max_tokens, 1);
+  // the small row-group kernels carry the kv head count in a 12-bit field
+  if (small_rows_path(kv_kind, dim, (Hq / Hkv) * L) && Hkv >= (1 << kSmallRowsHkvBits))
+    return fail(TQ_ERR_UNSUPPORTED, "attention: %d kv heads (at most %d with <= 4 query rows per kv head)",
+                Hkv, (1 << kSmallRowsHkvBits) - 1);
   const SplitPlan sp = plan_splits(B, Hq, Hkv, L, T, dim, kv_kind == TQ_KV_PACKED);
   if (static_cast<int64_t>(B) * Hkv * sp.n_rg > kMaxGroups)
     return fail(TQ_ERR_UNSUPPORTED, "attention: %lld (batch, kv head, row group) groups > %d",
@@ -382,7 +371,7 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   p.rscale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
   // the staged row-group kernel leaves Hadamard partials in the rotated basis
-  p.merge_rot = (kv_kind == TQ_KV_PACKED && !prod && rot_kind == TQ_ROT_HADAMARD && stage_path() &&
+  p.merge_rot = (kv_kind == TQ_KV_PACKED && !prod && rot_kind == TQ_ROT_HADAMARD &&
                  small_rows_path(kv_kind, dim, (Hq / Hkv) * L))
                     ? 1
                     : 0;

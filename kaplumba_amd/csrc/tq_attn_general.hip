@@ -837,12 +837,7 @@ bool pow2(int d) { return d > 0 && (d & (d - 1)) == 0; }
 }  // namespace
 
 bool tile_rows_path(int kv_kind, int Dk, int Dv, int rows) {
-  // KAPLUMBA_TQ_TILE=0 keeps these shapes on the other kernels (comparisons)
-  static const bool enabled = [] {
-    const char* e = getenv("KAPLUMBA_TQ_TILE");
-    return !(e && e[0] == '0');
-  }();
-  return enabled && kv_kind == TQ_KV_PACKED && Dk == 128 && Dv == 128 && rows >= kTileMinRows;
+  return kv_kind == TQ_KV_PACKED && Dk == 128 && Dv == 128 && rows >= kTileMinRows;
 }
 
 int64_t general_workspace_bytes(int B, int Hq, int Hkv, int L, int Dk, int Dv, int64_t T, bool prod) {

@@ -16,20 +16,11 @@ namespace tq {
 
 template <int D, int KB>
 int launch_small_vb(const AttnParams& p, int vb, hipStream_t st) {
-  if (stage_path()) {
-    switch (vb) {
-      case 1: return launch_stage<D, KB, 1>(p, st);
-      case 2: return launch_stage<D, KB, 2>(p, st);
-      case 3: return launch_stage<D, KB, 3>(p, st);
-      case 4: return launch_stage<D, KB, 4>(p, st);
-    }
-    return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
-  }
   switch (vb) {
-    case 1: return launch_small<D, KB, 1>(p, st);
-    case 2: return launch_small<D, KB, 2>(p, st);
-    case 3: return launch_small<D, KB, 3>(p, st);
-    case 4: return launch_small<D, KB, 4>(p, st);
+    case 1: return launch_stage<D, KB, 1>(p, st);
+    case 2: return launch_stage<D, KB, 2>(p, st);
+    case 3: return launch_stage<D, KB, 3>(p, st);
+    case 4: return launch_stage<D, KB, 4>(p, st);
   }
   return fail(TQ_ERR_INVALID_ARGUMENT, "attention: v_bits %d not in 1..4", vb);
 }

@@ -47,7 +47,7 @@
 namespace tq {
 
 // Shape bits of attn_stage_kernel's `pack` argument.
-constexpr int kStageHkvBits = 12;  // bits 0..11: kv heads
+constexpr int kStageHkvBits = kSmallRowsHkvBits;  // bits 0..11: kv heads (the host rejects more)
 constexpr int kStageRShift = 12;   // bits 12..14: GQA group R (<= 4)
 constexpr int kStageLShift = 15;   // bits 15..17: query length L (<= 4)
 constexpr int kStageF16Norms = 1 << 18;

@@ -241,7 +241,16 @@ _WORKSPACES: Dict[tuple, torch.Tensor] = {}
 # Workspaces replaced by a larger one.  They are never freed: a HIP graph
 # captured while one of them was current still holds its address, and a replay
 # must not write into memory the allocator has handed to another tensor.
+# Sizes grow at least twofold per replacement, so the kept buffers add up to
+# less than the current one.
 _RETIRED_WORKSPACES: list = []
+
+
+def _grown_size(current: int, need: int) -> int:
+    """Size of the buffer that replaces one of ``current`` bytes (0: none) when
+    a call needs ``need`` bytes: at least 1 MiB, ``need``, and twice
+    ``current``."""
+    return max(need, 1 << 20, 2 * current)
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -251,15 +260,17 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     split partials), so one buffer serves every later call on that stream,
     whatever the shapes, and needs no initial contents; calls on other
     streams get their own.  A request beyond the current size allocates a
-    larger buffer and keeps the old one alive (see _RETIRED_WORKSPACES);
-    ``reserve_workspace`` sizes it once before graph capture.
+    larger buffer (at least twice the old size) and keeps the old one alive
+    (see _RETIRED_WORKSPACES); ``reserve_workspace`` sizes it once before
+    graph capture.
     """
     key = (str(device), torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _RETIRED_WORKSPACES.append(ws)
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        size = _grown_size(0 if ws is None else ws.numel(), nbytes)
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

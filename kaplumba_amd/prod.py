@@ -185,7 +185,7 @@ def attention_prod(queries: torch.Tensor, keys: TurboQuantProdState, v_norms: to
             causal=causal, mask=mask, seq_lens=seq_lens, seq_starts=seq_starts)
     out = torch.empty((B, Hq, L, D), dtype=queries.dtype, device=queries.device)
     lib = _lib.load()
-    ws = _workspace(queries.device, lib.tq_attention_workspace_size(B, Hq, Hkv, L, D, T))
+    ws = _workspace(queries.device, lib.tq_attention_prod_workspace_size(B, Hq, Hkv, L, D, T))
     rc = lib.tq_attention_prod(
         queries.data_ptr(), _lib.torch_dtype_code(queries.dtype), B, Hq, Hkv, L, D,
         queries.stride(0), queries.stride(1), queries.stride(2), float(scale),

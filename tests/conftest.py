@@ -33,3 +33,17 @@ def device():
     assert torch.cuda.is_available(), "GPU tests need a visible ROCm device"
     print(f"[gpu] {torch.cuda.get_device_name(0)}", flush=True)
     return torch.device("cuda", 0)
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Write the attention parity margins (max-abs, mean-rel per checked
+    output) as JSON lines to $TQ_MARGINS_OUT, when set."""
+    path = os.environ.get("TQ_MARGINS_OUT")
+    mod = sys.modules.get("tests.test_attention_gpu")
+    if not path or mod is None:
+        return
+    import json
+
+    with open(path, "w") as f:
+        for m in mod.MARGINS:
+            f.write(json.dumps(m) + "\n")

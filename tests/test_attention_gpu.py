@@ -25,6 +25,9 @@ TORCH_QDT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 
 MANT_BITS = {"f32": 23, "f16": 10, "bf16": 7}
+# every assert_close call's margins; conftest writes them out when
+# TQ_MARGINS_OUT names a file
+MARGINS = []
 
 
 def dtype_ulp(w: np.ndarray, qdt: str) -> np.ndarray:
@@ -42,6 +45,8 @@ def assert_close(got: torch.Tensor, want64: np.ndarray, qdt: str, label=""):
     n_ulp = int((err > MAX_ABS).sum())
     print(f"[{label}] max_abs={err.max():.3e} mean_rel={mean_rel:.3e} one-ulp-flips>2e-3: {n_ulp}",
           flush=True)
+    MARGINS.append({"label": label, "max_abs": float(err.max()), "mean_rel": float(mean_rel),
+                    "elements": int(err.size), "over_2e-3_within_one_ulp": n_ulp})
     assert (err <= tol).all(), (label, err.max(), float((err - tol).max()))
     assert mean_rel <= MEAN_REL, (label, mean_rel)
 
@@ -304,11 +309,13 @@ def test_graph_survives_a_larger_workspace(device):
     assert torch.equal(call(big_q, big_kv), big)
 
 
-def test_config1_full_size(device):
+@pytest.mark.parametrize("codebook", ["beta", "gaussian"])
+def test_config1_full_size(device, codebook):
     """Config 1: 32 q heads / 8 kv heads, d=128, 32768 tokens, 3-bit, bf16 query.
 
     The cache is written by the HIP append kernel (bit-exact vs the oracle)
-    and attention is checked against the float64 oracle at full size.
+    and attention is checked against the float64 oracle at full size, with
+    the reference's Beta codebook and with BASELINE's N(0,1) Lloyd-Max one.
     """
     rs, rk, rv, rq = (np.random.default_rng(s) for s in (1000, 1001, 1002, 1003))
     T = 32768
@@ -316,7 +323,9 @@ def test_config1_full_size(device):
     k = (rk.standard_normal((1, 8, T, 128)) * scale).astype(np.float16)
     v = (rv.standard_normal((1, 8, T, 128)) * scale).astype(np.float16)
     q = O.round_to_dtype(rq.standard_normal((1, 32, 1, 128)).astype(np.float32), "bf16")
-    kc, vc = ops.Codec(128, 3, 0), ops.Codec(128, 3, 1)
+    kc = ops.Codec(128, 3, 0, codebook_kind=codebook)
+    vc = ops.Codec(128, 3, 1, codebook_kind=codebook)
+    cb = O.beta_codebook(128, 3) if codebook == "beta" else O.gaussian_codebook(128, 3)
     bufs = []
     for x, c in ((k, kc), (v, vc)):
         pb = torch.zeros((1, 8, T, 12), dtype=torch.uint32, device=device)
@@ -325,15 +334,15 @@ def test_config1_full_size(device):
         bufs.append((pb, nb))
     (kp, kn), (vp, vn) = bufs
     kp_np, vp_np = kp.cpu().numpy().astype(np.uint32), vp.cpu().numpy().astype(np.uint32)
-    wkp, wkn = O.quantize_rht(k, 3, O.rht_signs(128, 0), O.beta_codebook(128, 3))
+    wkp, wkn = O.quantize_rht(k, 3, O.rht_signs(128, 0), cb)
     assert np.array_equal(kp_np, wkp) and np.array_equal(kn.cpu().numpy(), wkn)
     out = ops.attention_packed(q_tensor(q, "bf16", device), kn, kp, vn, vp, kc, vc,
                                1 / math.sqrt(128), False)
     want = O.attention(q, kp_np, kn.cpu().numpy(), vp_np, vn.cpu().numpy(), k_bits=3, v_bits=3,
-                       k_codebook=O.beta_codebook(128, 3), v_codebook=O.beta_codebook(128, 3),
+                       k_codebook=cb, v_codebook=cb,
                        rot_kind="hadamard", k_rot=O.rht_signs(128, 0), v_rot=O.rht_signs(128, 1),
                        scale=1 / math.sqrt(128), q_dtype="bf16")
-    assert_close(out, want, "bf16", "config1")
+    assert_close(out, want, "bf16", f"config1 full size, {codebook} codebook")
 
 
 @pytest.mark.parametrize("kvdt", ["f16", "bf16"])

@@ -87,6 +87,36 @@ def test_attention_rejects_unsupported_dim_and_bad_heads():
     assert lib.tq_attention(*args) == _lib.TQ_ERR_INVALID_ARGUMENT
 
 
+def test_attention_rejects_kv_heads_beyond_the_small_rows_field():
+    # decode with <= 4 query rows per kv head packs the kv head count into 12
+    # bits of a launch argument: 4096 kv heads are refused before any launch
+    # (the pointers are never dereferenced: the check precedes every HIP call)
+    lib = _lib.load()
+    fake = 1 << 20
+    args = [fake, 2, 2, 4096, 4096, 1, 128, 0, 0, 0, 0.1, 0, 0, None, None, None, None, 0, 3, 3,
+            fake, fake, 0, fake, fake, 16, 0, None, 0, fake, fake, 1 << 30, None]
+    assert lib.tq_attention(*args) == _lib.TQ_ERR_UNSUPPORTED
+    assert b"kv heads" in lib.tq_last_error()
+
+
+def test_workspace_growth_keeps_retired_buffers_bounded():
+    # a long decode asks for a larger workspace as T grows; replacements at
+    # least double, so the buffers kept alive for captured graphs add up to
+    # less than the current one
+    from kaplumba_amd import ops
+    lib = _lib.load()
+    for (B, Hq, Hkv, D) in ((1, 8, 1, 128), (1, 8, 1, 256), (1, 32, 8, 512), (4, 32, 8, 128)):
+        cur, retired, replacements = 0, 0, 0
+        for T in range(1, 128 * 1024 + 1, 97):
+            need = lib.tq_attention_workspace_size(B, Hq, Hkv, 1, D, T)
+            if need > cur:
+                retired += cur
+                cur = ops._grown_size(cur, need)
+                replacements += 1
+        assert retired <= cur, (B, Hq, Hkv, D, retired, cur)
+        assert replacements <= 16, replacements
+
+
 def _general_args(**kw):
     """tq_attention_general arguments of a B = 0 call (validated, nothing launched)."""
     a = dict(q=None, q_dtype=2, B=0, Hq=32, Hkv=8, L=1, k_dim=128, v_dim=64, sb=0, sh=0, sl=0,
@@ -122,10 +152,14 @@ def test_general_attention_validates_without_the_gpu():
         args.update(kw)
         assert lib.tq_attention_general(*_general_args(**args)) == code, kw
         assert text in lib.tq_last_error(), (kw, lib.tq_last_error())
-    # the workspace query covers the tuned entry point's shapes too
+    # the workspace queries cover the general kernels, where the tuned entry
+    # points route shapes outside their kernels (Prod keys need the projected
+    # queries too)
     assert lib.tq_attention_general_workspace_size(1, 32, 8, 1, 128, 64, 4096) > 0
-    assert lib.tq_attention_workspace_size(1, 32, 8, 1, 512, 4096) >= \
+    assert lib.tq_attention_prod_workspace_size(1, 32, 8, 1, 512, 4096) >= \
         lib.tq_attention_general_workspace_size(1, 32, 8, 1, 512, 512, 4096)
+    assert lib.tq_attention_prod_workspace_size(1, 32, 8, 1, 512, 4096) > \
+        lib.tq_attention_workspace_size(1, 32, 8, 1, 512, 4096)
 
 
 def test_check_maps_status_to_exceptions():

@@ -34,7 +34,13 @@ def test_rotation_orthogonal_and_sign_fixed(d):
     assert abs(abs(np.linalg.det(R)) - 1.0) < 1e-3
     # sign fix: Q' = Q diag(sign(diag r)) makes diag(Q'^T M) = |diag r| > 0
     M = np.random.default_rng(0 + d * 7919).standard_normal((d, d), dtype=np.float32)
-    assert (np.diag(R.T @ M.astype(np.float64)) > 0).all()
+    U = R.T @ M.astype(np.float64)
+    assert (np.diag(U) > 0).all()
+    # R is the Q factor of exactly that draw: R^T M is upper triangular (a
+    # transposed R, another seed, or a missing sign fix all leave a full or
+    # negative-diagonal product)
+    assert np.abs(np.tril(U, -1)).max() < 1e-3 * np.abs(U).max()
+    assert np.abs(np.triu(U)).max() > 1.0
 
 
 # --------------------------------------------------------------- codebooks ---
