@@ -42,7 +42,8 @@ __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, xor_lane<2>(x));
   x = fmaxf(x, xor_lane<4>(x));
   x = fmaxf(x, xor_lane<8>(x));
-  x = fmaxf(x, xor_lane<16>(x));
+  const float2 r = rows16_pair(x);
+  x = fmaxf(r.x, r.y);
   const float2 h = halves(x);
   return fmaxf(h.x, h.y);
 }
@@ -69,7 +70,8 @@ __device__ __forceinline__ void wave_fwht(float (&y)[D / kWave], const float (&s
     v = fmaf(sgn[1], v, xor_lane<2>(v));
     v = fmaf(sgn[2], v, xor_lane<4>(v));
     v = fmaf(sgn[3], v, xor_lane<8>(v));
-    v = fmaf(sgn[4], v, xor_lane<16>(v));
+    const float2 r = rows16_pair(v);  // even rows: v + v[l + 16]; odd: v[l - 16] - v
+    v = fmaf(sgn[4], r.y, r.x);
     const float2 h = halves(v);  // lanes < 32: v + v[l + 32]; others: v[l - 32] - v
     y[e] = fmaf(sgn[5], h.y, h.x);
   }

@@ -84,12 +84,11 @@ struct StageShape {
   //      [query rows as loaded][key signs][slots: wave w owns NS consecutive]
   static constexpr int LUTK_OFF = 0;
   static constexpr int LUTV_OFF = KTAB;
-  static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [p][r][h][i] 8 x f16 = 16 B
+  static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [i][p][r][h] 8 x f16 = 16 B
   static constexpr int QST_BYTES = 2 * NQ * 2 * (D / 8) * 16;
   static constexpr int ZERO_OFF = QST_OFF + QST_BYTES;
-  static constexpr int QY_OFF = ZERO_OFF + 16;  // [NQ][D] f32
-  static constexpr int QMAX_OFF = QY_OFF + NQ * D * 4;
-  static constexpr int QRAW_OFF = QMAX_OFF + 16;           // [NQ][D] query rows as loaded (<= 4 B each)
+  static constexpr int QSC_OFF = ZERO_OFF + 16;            // [NQ] f32 hi/lo scale of each query row
+  static constexpr int QRAW_OFF = QSC_OFF + 16;            // [NQ][D] query rows as loaded (<= 4 B each)
   static constexpr int QSGN_OFF = QRAW_OFF + NQ * D * 4;    // [NQ][D] f32 key signs (one copy per query wave)
   static constexpr int SLOT_OFF = QSGN_OFF + NQ * D * 4;
   // 8 waves (two per SIMD), each with NS = 2 slots in flight.  Measured on
@@ -348,7 +347,12 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   if (tid < 4) reinterpret_cast<uint32_t*>(lds + S::ZERO_OFF)[tid] = 0u;
 
   // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
-  // (dense: rotated by qprep_kernel), into LDS with the row's max |y|
+  // (dense: rotated by qprep_kernel).  Query wave r splits its row into f16
+  // hi and lo pieces at the row's own scale (a power of two from max |y|) and
+  // writes them straight into the B-operand staging [jj][p][r][h]: as f16
+  // pairs, (q01, q01, q23, q23) of coordinates h D/2 + 4 jj + 0..3 of piece p.
+  // The 16 entries of one jj are contiguous, so the lanes' reads of one
+  // operand hit distinct banks.
   if (qwave) {
     // this wave's row and sign loads were issued before its NS * DMA_PER_SLOT
     // staged loads
@@ -371,37 +375,29 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
       for (int e = 0; e < QE; ++e) y[e] *= p.rscale;
     }
     float m = 0.f;
-    float* qy = reinterpret_cast<float*>(lds + S::QY_OFF) + wave * D;
+#pragma unroll
+    for (int e = 0; e < QE; ++e) m = fmaxf(m, fabsf(y[e]));
+    const float sq_row = f16_split_scale(wave_max(m));
+    if (lane == 0) reinterpret_cast<float*>(lds + S::QSC_OFF)[wave] = sq_row;
+    uint32_t* st = reinterpret_cast<uint32_t*>(lds + S::QST_OFF);
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
-      qy[lane + e * kWave] = y[e];
-      m = fmaxf(m, fabsf(y[e]));
+      uint32_t hi, lo;
+      split_f16(y[e] * sq_row, hi, lo);
+      // lanes 2k, 2k + 1 hold the two coordinates of one f16 pair
+      const uint32_t hi_n = __float_as_uint(xor_lane<1>(__uint_as_float(hi)));
+      const uint32_t lo_n = __float_as_uint(xor_lane<1>(__uint_as_float(lo)));
+      if ((lane & 1) == 0) {
+        const int c = lane + e * kWave;
+        const int h = c / (D / 2);
+        const int jj = (c % (D / 2)) / 4;  // 4-coordinate group
+        const int e2 = (c % 4) / 2;        // pair within the group
+        const int base0 = (((jj * 2 + 0) * NQ + wave) * 2 + h) * 4 + 2 * e2;
+        const int base1 = (((jj * 2 + 1) * NQ + wave) * 2 + h) * 4 + 2 * e2;
+        st[base0] = st[base0 + 1] = hi | (hi_n << 16);
+        st[base1] = st[base1 + 1] = lo | (lo_n << 16);
+      }
     }
-    m = wave_max(m);
-    if (lane == 0) reinterpret_cast<float*>(lds + S::QMAX_OFF)[wave] = m;
-  }
-  lds_only_barrier();
-  // query pieces in B-operand order: staging [p][r][h][jj] holds, as f16
-  // pairs, (q01, q01, q23, q23) of coordinates h D/2 + 4 jj + 0..3 of piece p
-  // of row r (one hi/lo scale for all rows)
-  const float* qmaxs = reinterpret_cast<const float*>(lds + S::QMAX_OFF);
-  const float sq = f16_split_scale(fmaxf(fmaxf(qmaxs[0], qmaxs[1]), fmaxf(qmaxs[2], qmaxs[3])));
-  for (int idx = tid; idx < NQ * D / 2; idx += NT) {
-    const int r = idx / (D / 2);
-    const int c = (idx % (D / 2)) * 2;
-    const float2 qq = reinterpret_cast<const float2*>(lds + S::QY_OFF)[idx];
-    uint32_t hi0, lo0, hi1, lo1;
-    split_f16(qq.x * sq, hi0, lo0);
-    split_f16(qq.y * sq, hi1, lo1);
-    const int h = c / (D / 2);
-    const int jj = (c % (D / 2)) / 4;   // 4-coordinate group
-    const int e = (c % 4) / 2;          // pair within the group
-    uint32_t* st = reinterpret_cast<uint32_t*>(lds + S::QST_OFF);
-    // [p][r][h][jj] = (pair0, pair0, pair1, pair1)
-    const int base0 = (((0 * NQ + r) * 2 + h) * (D / 8) + jj) * 4 + 2 * e;
-    const int base1 = (((1 * NQ + r) * 2 + h) * (D / 8) + jj) * 4 + 2 * e;
-    st[base0] = st[base0 + 1] = hi0 | (hi1 << 16);
-    st[base1] = st[base1 + 1] = lo0 | (lo1 << 16);
   }
   lds_only_barrier();
 
@@ -413,9 +409,9 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   u32x4_t qd[D / 8];
   {
     const uint32_t qb_addr = ((g >> 1) == jq)
-                                 ? static_cast<uint32_t>(S::QST_OFF + ((((n >> 3) * NQ + rq) * 2 + (g & 1)) * (D / 8)) * 16)
+                                 ? static_cast<uint32_t>(S::QST_OFF + (((n >> 3) * NQ + rq) * 2 + (g & 1)) * 16)
                                  : static_cast<uint32_t>(S::ZERO_OFF);
-    const uint32_t qb_step = ((g >> 1) == jq) ? 16u : 0u;
+    const uint32_t qb_step = ((g >> 1) == jq) ? 2u * NQ * 2 * 16 : 0u;
 #pragma unroll
     for (int j = 0; j < D / 8; ++j) qd[j] = lds_at<u32x4_t>(lds, qb_addr + j * qb_step);
   }
@@ -433,7 +429,8 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   uint32_t vmask = (S::VKEYS - 1u) << S::LOGSV;
   asm volatile("" : "+s"(kmask), "+s"(vmask));
   // score scale: S * ||k|| * log2(e) / (s_K s_Q) in log2 units
-  const float kscale = 1.4426950408889634f * __builtin_amdgcn_rcpf(sk) * __builtin_amdgcn_rcpf(sq);
+  const float kscale = 1.4426950408889634f * __builtin_amdgcn_rcpf(sk) *
+                       __builtin_amdgcn_rcpf(reinterpret_cast<const float*>(lds + S::QSC_OFF)[rq]);
   // causal limit of this lane's row (keys t <= lim are visible)
   int lim = INT32_MAX, lim_min = INT32_MAX;
   if (p.causal) {

@@ -166,17 +166,42 @@ __device__ __forceinline__ bool qb_entry(int t, const float* mid, int nmid, uint
   return inside <= 1;
 }
 
-// Lane value of the partner lane ^ OFF (OFF < 32): DPP inside a quad, a
-// swizzle beyond.
+// Lane value of the partner lane ^ OFF (OFF < 32), all in the vector ALU
+// (no LDS round trip): DPP inside a row of 16 lanes, the gfx950 row swap
+// across rows.
+//   1, 2: quad_perm [1,0,3,2], [2,3,0,1]
+//   4:    row_half_mirror (lane j of 8 <- 7 - j, i.e. ^7), then quad_perm
+//         [3,2,1,0] (^3): ^7 ^3 = ^4
+//   8:    row_ror:8 (lane j of 16 <- j + 8 mod 16 = j ^ 8)
+//   16:   v_permlane16_swap of the value with itself gives rows (0,0,2,2) and
+//         (1,1,3,3); the partner is the other one
 template <int OFF>
 __device__ __forceinline__ float xor_lane(float v) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16, "lane xor distance");
   const int x = __float_as_int(v);
-  if constexpr (OFF == 1)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, true));  // quad_perm [1,0,3,2]
-  else if constexpr (OFF == 2)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, true));  // quad_perm [2,3,0,1]
-  else
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1f | (OFF << 10)));  // bit mode: lane ^ OFF
+  if constexpr (OFF == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, true));
+  } else if constexpr (OFF == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, true));
+  } else if constexpr (OFF == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, true);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xf, 0xf, true));
+  } else if constexpr (OFF == 8) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, true));
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false, false);
+    return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+  }
+}
+
+// Rows of 16 lanes exchanged in pairs (v_permlane16_swap): .x = x of lane l
+// for even rows and of lane l - 16 for odd rows, .y = x of lane l + 16 for
+// even rows and of lane l otherwise; op(.x, .y) is the pairwise op of lanes
+// l, l ^ 16, and fma(s, .y, .x) with s = -1 on odd rows is the butterfly
+// (x_l + x_l^16 on even rows, x_l^16 - x_l on odd).
+__device__ __forceinline__ float2 rows16_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // ----------------------------------------------------------- bit fields ----
