@@ -466,7 +466,12 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   for (int i = 0; i < n_my; ++i) {
     const int s0 = sub_start(i);
     // this slot's transfers are complete once at most the other slots' remain
-    wait_vmcnt<(NS - 1) * S::DMA_PER_SLOT>();
+    // (sub-chunks past the wave's last are never staged, so near the end
+    // fewer slots are in flight)
+    if (i + NS - 1 < n_my)
+      wait_vmcnt<(NS - 1) * S::DMA_PER_SLOT>();
+    else
+      wait_vmcnt<0>();
     const unsigned char* sl = slots + slot * S::SLOT;
     uint32_t kw[KW];
     {
@@ -517,7 +522,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
       for (int w = 0; w < VRAW; ++w) asm volatile("" ::"v"(vw[e][w]));
 #pragma unroll
     for (int e = 0; e < 4; ++e) asm volatile("" ::"v"(nk[e]), "v"(nv[e]));
-    stage(slot, sub_start(i + NS));
+    if (i + NS < n_my) stage(slot, sub_start(i + NS));
     slot = slot + 1 == NS ? 0 : slot + 1;
 
     // ---- scores: D / 8 MFMAs in two alternating accumulator chains; the
@@ -659,7 +664,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
       }
     }
   }
-  // the trailing transfers (past t_end: zeros) land before the workgroup ends
+  // every staged transfer has landed (waves without sub-chunks wait here)
   wait_vmcnt<0>();
 
   // --------------------------------------------------- combine the waves ----
