@@ -415,8 +415,8 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
     const dim3 rgrid(4, static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
     const int valid = (seq_starts || seq_lens) ? -1 : static_cast<int>((T + sp.chunk - 1) / sp.chunk);
     switch (dim) {
-      case 64: hipLaunchKernelGGL(attn_merge_rot_kernel<64>, rgrid, dim3(kMergeThreads), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, p); break;
-      default: hipLaunchKernelGGL(attn_merge_rot_kernel<128>, rgrid, dim3(kMergeThreads), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, p); break;
+      case 64: hipLaunchKernelGGL(attn_merge_rot_kernel<64>, rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, Hkv, p); break;
+      default: hipLaunchKernelGGL(attn_merge_rot_kernel<128>, rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, Hkv, p); break;
     }
     return check_launch("attn_merge_rot_kernel");
   }

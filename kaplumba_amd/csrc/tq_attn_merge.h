@@ -48,6 +48,17 @@ __device__ __forceinline__ float wave_max(float x) {
   return fmaxf(h.x, h.y);
 }
 
+__device__ __forceinline__ float wave_sum(float x) {
+  x += xor_lane<1>(x);
+  x += xor_lane<2>(x);
+  x += xor_lane<4>(x);
+  x += xor_lane<8>(x);
+  const float2 r = rows16_pair(x);
+  x = r.x + r.y;
+  const float2 h = halves(x);
+  return h.x + h.y;
+}
+
 // Unnormalised Walsh-Hadamard transform of a D-vector held by one wave as
 // y[e] = x[lane + 64 e]: butterflies across e in-lane, across lanes by DPP,
 // swizzles and the half swap.  sgn[k] = -1 where lane bit k is set, else 1.

@@ -159,28 +159,26 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p)
 
 // Merge of the staged row-group kernel's splits (tq_attn_stage.h): 4-row
 // groups, Hadamard partials still in the rotated basis.  The hot arguments
-// (partial buffers, split counts, R_V's signs) come first and are preloaded
+// (partial buffers, split counts, R_V's signs, kv heads) come first and are preloaded
 // into SGPRs, so the partial loads go out without waiting for the argument
 // segment; valid = the split count of a sequence when no per-sequence
-// windows exist (-1: from seq_window).  Workgroup = one query row of one
-// (sequence, kv head); thread (float4 column c, split group sg) folds the
-// splits sg, sg + SG, ... by log-sum-exp with all its loads in flight, the
-// groups fold through LDS, and one wave applies R_V^-1 to the normalised row.
-template <int D>
-__global__ __launch_bounds__(kMergeThreads) void attn_merge_rot_kernel(const float* po, const float* pml,
-                                                                       const float* vrot, int n_splits,
-                                                                       int valid, AttnParams p) {
-  constexpr int NQ = 4;
-  constexpr int C4 = D / 4;
-  constexpr int SG = kMergeThreads / C4;  // split groups
-  constexpr int BATCH = 8;                 // splits per thread per round trip
-  constexpr int QE = D / kWave;
-  static_assert(kMergeThreads % C4 == 0, "merge mapping");
-  __shared__ float4 s_po[SG][C4];
-  __shared__ float s_pm[SG], s_pl[SG];
-  __shared__ float s_y[D];
+// windows exist (-1: from seq_window).  Workgroup = one wave = one query row
+// of one (sequence, kv head); lane l owns coordinates l + 64 e.  Lane u
+// loads split u's (m, l) and every lane its o values of the MB splits, all
+// loads in flight at once; the log-sum-exp weights come from wave
+// reductions and reach every lane by readlane, so the fold needs no LDS and
+// no barrier (longer rows fold MB splits per round trip).  R_V^-1 is a wave
+// Walsh-Hadamard transform; the row is stored in the query dtype.
+constexpr int kMergeRotSplits = 32;  // splits per round trip of attn_merge_rot_kernel
 
-  const int tid = threadIdx.x;
+template <int D>
+__global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, const float* pml,
+                                                               const float* vrot, int n_splits,
+                                                               int valid, int hkv, AttnParams p) {
+  constexpr int NQ = 4;
+  constexpr int QE = D / kWave;
+  constexpr int MB = kMergeRotSplits;
+  const int lane = threadIdx.x;
   const int j = blockIdx.x;
   const int gk = blockIdx.y;
   const int b = blockIdx.z;
@@ -189,90 +187,57 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_rot_kernel(const flo
     return win.len > 0 ? static_cast<int>((win.len + p.chunk - 1) / p.chunk) : 0;
   }();
   if (nvalid <= 1) return;  // the partial kernel wrote these rows itself
-  const int64_t grp = static_cast<int64_t>(b) * gridDim.y + gk;
+  const int64_t grp = static_cast<int64_t>(b) * hkv + gk;  // (hkv preloaded: no wait for the grid size)
   const float* po_g = po + grp * static_cast<int64_t>(n_splits) * NQ * D;
-  const float* pml_g = pml + grp * static_cast<int64_t>(n_splits) * NQ * 2;
-  const int c = tid % C4;
-  const int sg = tid / C4;
-  // R_V^-1's signs, loaded with the partials (not after the fold: one round trip)
+  const float2* pml_g = reinterpret_cast<const float2*>(pml) + grp * static_cast<int64_t>(n_splits) * NQ;
+  // R_V^-1's signs, loaded with the partials
   float vr[QE];
 #pragma unroll
-  for (int e = 0; e < QE; ++e) vr[e] = tid < kWave ? vrot[tid + e * kWave] : 0.f;
+  for (int e = 0; e < QE; ++e) vr[e] = vrot[lane + e * kWave];
   float M = -INFINITY, Lsum = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp0 = sg; sp0 < nvalid; sp0 += SG * BATCH) {
-    float2 ml[BATCH];
-    float4 oo[BATCH];
+  float acc[QE];
 #pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const int sp = sp0 + u * SG;
-      if (sp < nvalid) {
-        const int64_t r = static_cast<int64_t>(sp) * NQ + j;
-        ml[u] = reinterpret_cast<const float2*>(pml_g)[r];
-        oo[u] = reinterpret_cast<const float4*>(po_g + r * D)[c];
-      } else {
-        ml[u] = make_float2(-INFINITY, 0.f);
-        oo[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+  for (int e = 0; e < QE; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < nvalid; s0 += MB) {
+    // lane u < MB holds split s0 + u's (m, l); every lane holds its o values
+    // of the MB splits (past the last split: a repeat of it, weighted 0)
+    const bool has = lane < MB && s0 + lane < nvalid;
+    const float2 mlu = has ? pml_g[static_cast<int64_t>(s0 + lane) * NQ + j] : make_float2(-INFINITY, 0.f);
+    float oo[MB][QE];
+#pragma unroll
+    for (int u = 0; u < MB; ++u) {
+      const int sp = s0 + u < nvalid ? s0 + u : nvalid - 1;
+#pragma unroll
+      for (int e = 0; e < QE; ++e) oo[u][e] = po_g[(static_cast<int64_t>(sp) * NQ + j) * D + lane + e * kWave];
     }
-    float bm = M;
+    const float bm = fmaxf(M, wave_max(mlu.x));
+    const float r0 = M == -INFINITY ? 0.f : __expf(M - bm);
+    const float w = mlu.x == -INFINITY ? 0.f : __expf(mlu.x - bm);
+    Lsum = fmaf(Lsum, r0, wave_sum(w * mlu.y));
 #pragma unroll
-    for (int u = 0; u < BATCH; ++u) bm = fmaxf(bm, ml[u].x);
-    const float r0 = (M == -INFINITY) ? 0.f : __expf(M - bm);
-    Lsum *= r0;
-    acc.x *= r0;
-    acc.y *= r0;
-    acc.z *= r0;
-    acc.w *= r0;
+    for (int e = 0; e < QE; ++e) acc[e] *= r0;
 #pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const float sc = (ml[u].x == -INFINITY) ? 0.f : __expf(ml[u].x - bm);
-      Lsum = fmaf(sc, ml[u].y, Lsum);
-      acc.x = fmaf(sc, oo[u].x, acc.x);
-      acc.y = fmaf(sc, oo[u].y, acc.y);
-      acc.z = fmaf(sc, oo[u].z, acc.z);
-      acc.w = fmaf(sc, oo[u].w, acc.w);
+    for (int u = 0; u < MB; ++u) {
+      const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+#pragma unroll
+      for (int e = 0; e < QE; ++e) acc[e] = fmaf(wu, oo[u][e], acc[e]);
     }
     M = bm;
   }
-  s_po[sg][c] = acc;
-  if (c == 0) {
-    s_pm[sg] = M;
-    s_pl[sg] = Lsum;
-  }
-  __syncthreads();
-  if (tid < C4) {
-    float Mt = -INFINITY;
+  const float inv = 1.f / fmaxf(Lsum, kNormEps);
+  float y[QE];
 #pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) Mt = fmaxf(Mt, s_pm[g2]);
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    float lt = 0.f;
+  for (int e = 0; e < QE; ++e) y[e] = acc[e] * inv;
+  float sg6[6];
 #pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) {
-      const float sc = (s_pm[g2] == -INFINITY) ? 0.f : __expf(s_pm[g2] - Mt);
-      lt = fmaf(sc, s_pl[g2], lt);
-      a.x = fmaf(sc, s_po[g2][tid].x, a.x);
-      a.y = fmaf(sc, s_po[g2][tid].y, a.y);
-      a.z = fmaf(sc, s_po[g2][tid].z, a.z);
-      a.w = fmaf(sc, s_po[g2][tid].w, a.w);
-    }
-    const float inv = 1.f / fmaxf(lt, kNormEps);
-    reinterpret_cast<float4*>(s_y)[tid] = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
-  }
-  __syncthreads();
-  if (tid < kWave && j < p.R * p.L) {
-    float sg6[6];
+  for (int k = 0; k < 6; ++k) sg6[k] = (lane >> k) & 1 ? -1.f : 1.f;
+  wave_fwht<D>(y, sg6);
+  // (rows past the group's last exist in the partials but not in the output;
+  // checked only here, so the partial loads above go out first)
+  if (j >= p.R * p.L) return;
+  const int64_t qo = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + j / p.L) * p.L + j % p.L) * D;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) sg6[k] = (tid >> k) & 1 ? -1.f : 1.f;
-    float y[QE];
-#pragma unroll
-    for (int e = 0; e < QE; ++e) y[e] = s_y[tid + e * kWave];
-    wave_fwht<D>(y, sg6);
-    const int64_t qo = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + j / p.L) * p.L + j % p.L) * D;
-#pragma unroll
-    for (int e = 0; e < QE; ++e)
-      store_out(p.out, p.q_dtype, qo + tid + e * kWave, y[e] * p.rscale * vr[e]);
-  }
+  for (int e = 0; e < QE; ++e) store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * vr[e]);
 }
 
 }  // namespace tq
