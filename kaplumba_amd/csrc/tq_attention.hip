@@ -549,3 +549,10 @@ extern "C" int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int 
                         capacity, max_tokens, seq_starts, seq_lens, causal, out, workspace,
                         workspace_bytes_given, stream, &pk);
 }
+
+#ifdef TQ_PHASE_STAMPS
+// Phase stamps of the last attn_merge_rot_kernel launch (stamps build only).
+extern "C" int tq_dbg_merge_stamps(void* dst, long long bytes) {
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(tq::g_merge_stamps), bytes) == hipSuccess ? 0 : 1;
+}
+#endif

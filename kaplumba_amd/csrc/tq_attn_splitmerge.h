@@ -18,6 +18,24 @@
 
 #include "tq_attn_merge.h"
 
+// Phase stamps of attn_merge_rot_kernel (build option TQ_PHASE_STAMPS, read
+// with tq_dbg_merge_stamps()): rows 0 entry, 1 loads in, 2 folded, 3 stored.
+#ifdef TQ_PHASE_STAMPS
+namespace tq {
+static __device__ uint64_t g_merge_stamps[4][1024];
+}
+#define MERGE_STAMP(i)                                                                            \
+  do {                                                                                            \
+    if (threadIdx.x == 0)                                                                         \
+      g_merge_stamps[i][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] =         \
+          __builtin_amdgcn_s_memrealtime();                                                       \
+  } while (0)
+#else
+#define MERGE_STAMP(i) \
+  do {               \
+  } while (0)
+#endif
+
 namespace tq {
 
 constexpr int kMergeThreads = 256;
@@ -182,6 +200,7 @@ __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, 
   const int j = blockIdx.x;
   const int gk = blockIdx.y;
   const int b = blockIdx.z;
+  MERGE_STAMP(0);
   const int nvalid = valid >= 0 ? valid : [&] {
     const SeqWindow win = seq_window(p, b);
     return win.len > 0 ? static_cast<int>((win.len + p.chunk - 1) / p.chunk) : 0;
@@ -210,6 +229,7 @@ __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, 
 #pragma unroll
       for (int e = 0; e < QE; ++e) oo[u][e] = po_g[(static_cast<int64_t>(sp) * NQ + j) * D + lane + e * kWave];
     }
+    if (s0 == 0) MERGE_STAMP(1);
     const float bm = fmaxf(M, wave_max(mlu.x));
     const float r0 = M == -INFINITY ? 0.f : __expf(M - bm);
     const float w = mlu.x == -INFINITY ? 0.f : __expf(mlu.x - bm);
@@ -224,6 +244,7 @@ __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, 
     }
     M = bm;
   }
+  MERGE_STAMP(2);
   const float inv = 1.f / fmaxf(Lsum, kNormEps);
   float y[QE];
 #pragma unroll
@@ -238,6 +259,7 @@ __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, 
   const int64_t qo = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + j / p.L) * p.L + j % p.L) * D;
 #pragma unroll
   for (int e = 0; e < QE; ++e) store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * vr[e]);
+  MERGE_STAMP(3);
 }
 
 }  // namespace tq

@@ -44,6 +44,39 @@
 
 #include "tq_attn_small.h"
 
+// Phase stamps (build option TQ_PHASE_STAMPS; the shipped library has none):
+// the 100 MHz wall clock at the phase boundaries of attn_stage_kernel,
+// thread 0 of a workgroup (STAGE_STAMP) or lane 0 of every wave
+// (STAGE_WSTAMP, rows r + wave), read back with tq_dbg_stage_stamps() from
+// libkaplumba_tq_stamps.so (make -C kaplumba_amd/csrc stamps).  Rows:
+// 0 entry, 1 codebooks in registers, 2 tables stored, 3 query row in LDS,
+// 4 query staged, 5 staging barrier, 6 query operands loaded, 8+w loop start,
+// 16+w first slot ready, 24+w loop end, 32 combine barrier, 33 partial stored.
+#ifdef TQ_PHASE_STAMPS
+namespace tq {
+static __device__ uint64_t g_stage_stamps[40][1024];
+}
+#define STAGE_STAMP(i)                                                                              \
+  do {                                                                                              \
+    if (threadIdx.x == 0)                                                                           \
+      g_stage_stamps[i][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] =           \
+          __builtin_amdgcn_s_memrealtime();                                                         \
+  } while (0)
+#define STAGE_WSTAMP(i)                                                                             \
+  do {                                                                                              \
+    if ((threadIdx.x & 63) == 0)                                                                    \
+      g_stage_stamps[(i) + threadIdx.x / 64][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = \
+          __builtin_amdgcn_s_memrealtime();                                                         \
+  } while (0)
+#else
+#define STAGE_STAMP(i) \
+  do {               \
+  } while (0)
+#define STAGE_WSTAMP(i) \
+  do {                \
+  } while (0)
+#endif
+
 namespace tq {
 
 // Shape bits of attn_stage_kernel's `pack` argument.
@@ -213,6 +246,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   const int gk = blockIdx.y;
   const int b = blockIdx.z;
   const int Hkv = pack & ((1 << kStageHkvBits) - 1);
+  STAGE_STAMP(0);
   const int R = (pack >> kStageRShift) & 7;
   const int L = (pack >> kStageLShift) & 7;
   const int nrows = R * L;
@@ -320,6 +354,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   for (int i = 0; i < (1 << KB); ++i) kmax = fmaxf(kmax, fabsf(ckb[i]));
 #pragma unroll
   for (int i = 0; i < (1 << VB); ++i) vmax = fmaxf(vmax, fabsf(cvb[i]));
+  STAGE_STAMP(1);
   const float sk = f16_split_scale(kmax);
   const float cbs_v = f16_split_scale(vmax);
   {
@@ -345,6 +380,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     }
   }
   if (tid < 4) reinterpret_cast<uint32_t*>(lds + S::ZERO_OFF)[tid] = 0u;
+  STAGE_STAMP(2);
 
   // ---- query rows: q_s = round_qdtype(q * scale_q) * s_K, Hadamard, * 1/sqrt(D)
   // (dense: rotated by qprep_kernel).  Query wave r splits its row into f16
@@ -357,6 +393,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     // this wave's row and sign loads were issued before its NS * DMA_PER_SLOT
     // staged loads
     wait_vmcnt<NS * S::DMA_PER_SLOT>();
+    STAGE_STAMP(3);
     float y[QE];
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
@@ -379,6 +416,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     for (int e = 0; e < QE; ++e) m = fmaxf(m, fabsf(y[e]));
     const float sq_row = f16_split_scale(wave_max(m));
     if (lane == 0) reinterpret_cast<float*>(lds + S::QSC_OFF)[wave] = sq_row;
+    STAGE_STAMP(4);
     uint32_t* st = reinterpret_cast<uint32_t*>(lds + S::QST_OFF);
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
@@ -400,6 +438,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     }
   }
   lds_only_barrier();
+  STAGE_STAMP(5);
 
   // ---- lane constants
   const int jq = (n >> 2) & 1;  // token subset of this lane's score column
@@ -415,6 +454,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
 #pragma unroll
     for (int j = 0; j < D / 8; ++j) qd[j] = lds_at<u32x4_t>(lds, qb_addr + j * qb_step);
   }
+  STAGE_STAMP(6);
   // keys: token 16 (g >> 1) + n, half g & 1 of the slot's rows
   const uint32_t k_lane = (16 * (g >> 1) + n) * (PWK * 4) + (g & 1) * (KW * 4);
   // norms: tokens 16 jq + 4 g .. + 3 of the sub-chunk
@@ -462,9 +502,23 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   }();
 
   int slot = 0;  // i % NS
+  STAGE_WSTAMP(8);
 #pragma unroll 1
   for (int i = 0; i < n_my; ++i) {
     const int s0 = sub_start(i);
+    // Issue priority falls as a wave advances.  Two waves share a SIMD, and
+    // at equal priority the older one (waves 0-3) is picked first: it ran
+    // ahead and finished about one sub-chunk early, leaving the younger one
+    // alone on the SIMD for its last sub-chunk.  A wave that is behind now
+    // takes precedence, so the pair stays level and overlaps to the end.
+    if (i == 0)
+      __builtin_amdgcn_s_setprio(3);
+    else if (i == 1)
+      __builtin_amdgcn_s_setprio(2);
+    else if (i == 2)
+      __builtin_amdgcn_s_setprio(1);
+    else
+      __builtin_amdgcn_s_setprio(0);
     // this slot's transfers are complete once at most the other slots' remain
     // (sub-chunks past the wave's last are never staged, so near the end
     // fewer slots are in flight)
@@ -472,6 +526,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
       wait_vmcnt<(NS - 1) * S::DMA_PER_SLOT>();
     else
       wait_vmcnt<0>();
+    if (i == 0) STAGE_WSTAMP(16);
     const unsigned char* sl = slots + slot * S::SLOT;
     uint32_t kw[KW];
     {
@@ -664,8 +719,10 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
       }
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   // every staged transfer has landed (waves without sub-chunks wait here)
   wait_vmcnt<0>();
+  STAGE_WSTAMP(24);
 
   // --------------------------------------------------- combine the waves ----
   // l of row r: lanes (g', n) with n < 8 (piece 0), subsets n and n + 4
@@ -676,6 +733,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
     lr = h.x + h.y;
   }
   lds_barrier();  // every wave is done with the tables and staging
+  STAGE_STAMP(32);
   float* s_wo = reinterpret_cast<float*>(lds + S::WO_OFF);
   float* s_wm = reinterpret_cast<float*>(lds + S::WM_OFF);
   float* s_wl = reinterpret_cast<float*>(lds + S::WL_OFF);
@@ -725,6 +783,7 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
       s_fo[idx] = lt > 0.f ? a / lt : 0.f;  // 0 when no token is visible
     }
   }
+  STAGE_STAMP(33);
   if (nvalid > 1) return;
 
   // ---- finish a single split: R_V^-1, store
