@@ -506,19 +506,8 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
 #pragma unroll 1
   for (int i = 0; i < n_my; ++i) {
     const int s0 = sub_start(i);
-    // Issue priority falls as a wave advances.  Two waves share a SIMD, and
-    // at equal priority the older one (waves 0-3) is picked first: it ran
-    // ahead and finished about one sub-chunk early, leaving the younger one
-    // alone on the SIMD for its last sub-chunk.  A wave that is behind now
-    // takes precedence, so the pair stays level and overlaps to the end.
-    if (i == 0)
-      __builtin_amdgcn_s_setprio(3);
-    else if (i == 1)
-      __builtin_amdgcn_s_setprio(2);
-    else if (i == 2)
-      __builtin_amdgcn_s_setprio(1);
-    else
-      __builtin_amdgcn_s_setprio(0);
+    // (without it, waves 0-3 finished about one sub-chunk before 4-7)
+    prio_by_progress(i, n_my);
     // this slot's transfers are complete once at most the other slots' remain
     // (sub-chunks past the wave's last are never staged, so near the end
     // fewer slots are in flight)

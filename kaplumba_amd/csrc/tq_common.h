@@ -204,6 +204,24 @@ __device__ __forceinline__ float2 rows16_pair(float x) {
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Issue priority from a wave's progress through its n loop steps: 3 at the
+// start down to 0 in the last quarter (uniform arithmetic; s_setprio takes
+// an immediate).  Two waves share a SIMD, and at equal priority the older is
+// picked first, runs ahead and leaves the younger alone on the SIMD at the
+// end; with priority falling as a wave advances, the one behind takes
+// precedence and the pair stays level.
+__device__ __forceinline__ void prio_by_progress(int i, int n) {
+  const int left4 = 4 * (n - i);
+  if (left4 > 3 * n)
+    __builtin_amdgcn_s_setprio(3);
+  else if (left4 > 2 * n)
+    __builtin_amdgcn_s_setprio(2);
+  else if (left4 > n)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // ----------------------------------------------------------- bit fields ----
 // Value of bits [pos, pos+nb) of a little-endian word array held in registers.
 // pos and nb are compile-time after unrolling, so this folds to v_bfe_u32 or
