@@ -36,6 +36,9 @@
 
 namespace tq {
 
+// log2 of a power of two
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
+
 template <int KB, int VB>
 struct Rows16Shape {
   static constexpr int D = 128;
@@ -49,22 +52,35 @@ struct Rows16Shape {
   static constexpr int KW = QTR * KB / 32;  // words per token and lane
   static constexpr int PWK = D * KB / 32;
   static constexpr int NKJ = D / 32;        // MFMAs per tile and key piece
-  static constexpr int KKEYS = 1 << (2 * KB);
-  static constexpr int REPK = KKEYS <= 64 ? 64 : 16;
-  static constexpr int LOGSK = REPK == 64 ? 8 : 6;  // log2(REPK * 4)
+  // A key-table read covers KCO coordinates of one token: four at 1 and 2
+  // bits (8-byte entries of four f16), else two (4-byte entries).
+  static constexpr bool QUADK = KB <= 2;
+  static constexpr int KCO = QUADK ? 4 : 2;
+  static constexpr int KEB = 2 * KCO;  // bytes per hi or lo entry
+  static constexpr int KKEYS = 1 << (KCO * KB);
+  static constexpr int REPK = QUADK ? (KKEYS <= 16 ? 32 : 16) : (KKEYS <= 64 ? 64 : 16);
+  static constexpr int LOGSK = ilog2(REPK * KEB);
   // values: a lane holds CPL consecutive coordinates of 8 tokens
   static constexpr int CPL = D / 16;
   static constexpr int PWV = D * VB / 32;
   static constexpr int SEGBITS = CPL * VB;
   static constexpr int VRAW = (VB == 3) ? 2 : 1;
-  static constexpr int VKEYS = 1 << (2 * VB);
-  static constexpr int REPV = VKEYS <= 64 ? 64 : 16;
-  static constexpr int LOGSV = REPV == 64 ? 9 : 7;
-  // LDS (bytes): [K hi table][K lo table][V (hi, lo) table][q staging][rows][row max]
-  static constexpr int KTAB = KKEYS * REPK * 4;
+  // 1-bit values: v = m + h s with s = +-1 exact in f16, so the value
+  // operand needs no hi/lo split; a table read gives s of four tokens for one
+  // coordinate (16 keys, four f16).  Wider values: a read gives the (hi
+  // pair, lo pair) of two tokens' codebook values.
+  static constexpr bool SIGNV = VB == 1;
+  static constexpr int VKEYS = SIGNV ? 16 : 1 << (2 * VB);
+  static constexpr int REPV = SIGNV ? 32 : (VKEYS <= 64 ? 64 : 16);
+  static constexpr int LOGSV = ilog2(REPV * 8);
+  // LDS (bytes): [K hi table][K lo table][V table][q staging][rows][row max]
+  static constexpr int KTAB = KKEYS * REPK * KEB;
   static constexpr int VTAB = VKEYS * REPV * 8;
   static constexpr int LUTK_OFF = 0;
   static constexpr int LUTV_OFF = 2 * KTAB;
+  // A table offset beyond the 16-bit instruction offset goes into the lane
+  // base instead (by OR: the offset is a multiple of the table size).
+  static constexpr bool VOFF_IN_BASE = LUTV_OFF > 65535;
   static constexpr int QST_OFF = LUTV_OFF + VTAB;  // [piece][row][g][j] 8 x f16 = 16 B
   static constexpr int QST_BYTES = 2 * NQ * 4 * NKJ * 16;
   static constexpr int QY_OFF = QST_OFF + QST_BYTES;    // [NQ][D] f32 rotated queries
@@ -76,14 +92,16 @@ struct Rows16Shape {
   static constexpr int WL_OFF = WM_OFF + NW * NQ * 4;
   static constexpr int WE_OFF = WL_OFF + NW * NQ * 4;
   static constexpr int WF_OFF = WE_OFF + NW * NQ * 4;
-  static constexpr int FO_OFF = WF_OFF + NW * NQ * 4;      // [NQ][D] final rows
-  static constexpr int FL_OFF = FO_OFF + NQ * D * 4;       // [NQ] l, [NQ] m
-  static constexpr int POST_BYTES = FL_OFF + 2 * NQ * 4;
+  static constexpr int WV_OFF = WF_OFF + NW * NQ * 4;      // [NW][NQ] weight sums (1-bit values)
+  static constexpr int FO_OFF = WV_OFF + NW * NQ * 4;      // [NQ][D] final rows
+  static constexpr int FL_OFF = FO_OFF + NQ * D * 4;       // [NQ] l, [NQ] m, [NQ] v_mid term
+  static constexpr int POST_BYTES = FL_OFF + 3 * NQ * 4;
   static constexpr int BYTES = LOOP_BYTES > POST_BYTES ? LOOP_BYTES : POST_BYTES;
   static_assert(KW * 32 == QTR * KB, "key quarter rows are whole words");
   static_assert(SEGBITS <= 32, "value segment in one word");
   static_assert(BYTES <= 160 * 1024, "LDS per workgroup");
-  static_assert(LUTV_OFF < 65536, "table offsets fit the instruction offset field");
+  static_assert(LUTK_OFF + KTAB < 65536, "key tables fit the instruction offset field");
+  static_assert(!VOFF_IN_BASE || LUTV_OFF % VTAB == 0, "value table offset ORs into the lane base");
 };
 
 template <int KB, int VB>
@@ -154,8 +172,9 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   const int vbit = CPL * n * VB;
   const uint32_t v_lane = (vbit >> 5) * 4;
   const int vsh = vbit & 31;
-  const uint32_t lutk_lane = (lane % S::REPK) * 4;
-  const uint32_t lutv_lane = (lane % S::REPV) * 8;
+  const uint32_t lutk_lane = (lane % S::REPK) * S::KEB;
+  const uint32_t lutv_lane = (S::VOFF_IN_BASE ? S::LUTV_OFF : 0) + (lane % S::REPV) * 8;
+  constexpr int VOFF = S::VOFF_IN_BASE ? 0 : S::LUTV_OFF;  // instruction offset of value-table reads
   uint32_t kmask = (S::KKEYS - 1u) << S::LOGSK;
   uint32_t vmask = (S::VKEYS - 1u) << S::LOGSV;
   asm volatile("" : "+s"(kmask), "+s"(vmask));
@@ -186,11 +205,21 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
         bf.nv[t][e] = c[e];
       }
     }
-    const uint32_t vo = t0 * (PWV * 4) + v_lane;
+    if constexpr (S::SIGNV) {
+      // the lane's CPL = 8 one-bit fields of each token are byte n of the row
+      const uint32_t vo = t0 * (PWV * 4) + n;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int tok = (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
-      load_words<VRAW>(bf.v[e], vrs, vo + tok * (PWV * 4));
+      for (int e = 0; e < 8; ++e) {
+        const int tok = (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
+        bf.v[e][0] = __builtin_amdgcn_raw_buffer_load_b8(vrs, vo + tok * (PWV * 4), 0, 0);
+      }
+    } else {
+      const uint32_t vo = t0 * (PWV * 4) + v_lane;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tok = (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
+        load_words<VRAW>(bf.v[e], vrs, vo + tok * (PWV * 4));
+      }
     }
   };
   auto norm4 = [&](const uint32_t (&raw)[4], float (&x)[4]) {
@@ -255,29 +284,57 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   const float sk = f16_split_scale(kmax);
   const float cbs_v = f16_split_scale(vmax);
   static_assert(S::KKEYS * S::REPK / 8 <= NT && S::VKEYS * S::REPV / 8 <= NT, "one table slot per thread");
+  // a thread writes 8 consecutive replicas of one key
   {
     const int kslot = tid < S::KKEYS * S::REPK / 8 ? tid : 0;
     const int vslot = tid < S::VKEYS * S::REPV / 8 ? tid : 0;
     const int kkey = kslot / (S::REPK / 8), vkey = vslot / (S::REPV / 8);
-    const float cka = mux_pick<KB>(ckb, kkey & ((1 << KB) - 1)), ckb2 = mux_pick<KB>(ckb, kkey >> KB);
-    const float cva = mux_pick<VB>(cvb, vkey & ((1 << VB) - 1)), cvb2 = mux_pick<VB>(cvb, vkey >> VB);
-    if (tid < S::KKEYS * S::REPK / 8) {
-      uint32_t h0, l0, h1, l1;
-      split_f16(cka * sk, h0, l0);
-      split_f16(ckb2 * sk, h1, l1);
-      const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
-      uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + kslot * 2;
-      uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + kslot * 2;
-      dh[0] = dh[1] = make_uint4(hi, hi, hi, hi);
-      dl[0] = dl[1] = make_uint4(lo, lo, lo, lo);
+    if constexpr (S::QUADK) {
+      // key f0 | f1 << KB | f2 << 2 KB | f3 << 3 KB: f16 parts of c[f0] s .. c[f3] s
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) split_f16(mux_pick<KB>(ckb, (kkey >> (KB * i)) & ((1 << KB) - 1)) * sk, h[i], l[i]);
+      if (tid < S::KKEYS * S::REPK / 8) {
+        const uint32_t h01 = h[0] | (h[1] << 16), h23 = h[2] | (h[3] << 16);
+        const uint32_t l01 = l[0] | (l[1] << 16), l23 = l[2] | (l[3] << 16);
+        uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + kslot * 4;
+        uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + kslot * 4;
+        dh[0] = dh[1] = dh[2] = dh[3] = make_uint4(h01, h23, h01, h23);
+        dl[0] = dl[1] = dl[2] = dl[3] = make_uint4(l01, l23, l01, l23);
+      }
+    } else {
+      const float cka = mux_pick<KB>(ckb, kkey & ((1 << KB) - 1)), ckb2 = mux_pick<KB>(ckb, kkey >> KB);
+      if (tid < S::KKEYS * S::REPK / 8) {
+        uint32_t h0, l0, h1, l1;
+        split_f16(cka * sk, h0, l0);
+        split_f16(ckb2 * sk, h1, l1);
+        const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+        uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + kslot * 2;
+        uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + kslot * 2;
+        dh[0] = dh[1] = make_uint4(hi, hi, hi, hi);
+        dl[0] = dl[1] = make_uint4(lo, lo, lo, lo);
+      }
     }
-    if (tid < S::VKEYS * S::REPV / 8) {
-      uint32_t h0, l0, h1, l1;
-      split_f16(cva * cbs_v, h0, l0);
-      split_f16(cvb2 * cbs_v, h1, l1);
-      const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
-      uint4* d = reinterpret_cast<uint4*>(lds + S::LUTV_OFF) + vslot * 4;
-      d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
+    if constexpr (S::SIGNV) {
+      // entry e: s = +1 (f16 0x3c00) where bit e of the key is set, else -1 (0xbc00)
+      uint32_t sg[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sg[e] = (vkey >> e) & 1 ? 0x3c00u : 0xbc00u;
+      if (tid < S::VKEYS * S::REPV / 8) {
+        const uint32_t x = sg[0] | (sg[1] << 16), y = sg[2] | (sg[3] << 16);
+        uint4* d = reinterpret_cast<uint4*>(lds + S::LUTV_OFF) + vslot * 4;
+        d[0] = d[1] = d[2] = d[3] = make_uint4(x, y, x, y);
+      }
+    } else {
+      const float cva = mux_pick<VB>(cvb, vkey & ((1 << VB) - 1)), cvb2 = mux_pick<VB>(cvb, vkey >> VB);
+      if (tid < S::VKEYS * S::REPV / 8) {
+        uint32_t h0, l0, h1, l1;
+        split_f16(cva * cbs_v, h0, l0);
+        split_f16(cvb2 * cbs_v, h1, l1);
+        const uint32_t hi = h0 | (h1 << 16), lo = l0 | (l1 << 16);
+        uint4* d = reinterpret_cast<uint4*>(lds + S::LUTV_OFF) + vslot * 4;
+        d[0] = d[1] = d[2] = d[3] = make_uint4(hi, lo, hi, lo);
+      }
     }
   }
 
@@ -367,6 +424,11 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   float vsc = 0.f;          // 2^-E
   float nv_lim = 0.f;       // 2^(E + 8): larger norms could overflow an f16 weight
   float l_acc = 0.f;        // sum of p over this lane's tokens of row n
+  // 1-bit values: v = v_mid + v_half s.  Lw accumulates the f16 weights
+  // (row 4g + i in register i, every column alike) when v_mid != 0.
+  f32x4_t Lw = {0.f, 0.f, 0.f, 0.f};
+  const float v_mid = 0.5f * (cvb[0] + cvb[(1 << VB) - 1]);
+  const float v_half = 0.5f * (cvb[(1 << VB) - 1] - cvb[0]);
 
   struct Scores {
     f32x4_t c[2];
@@ -381,11 +443,22 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         u32x4_t ah, al;
+        if constexpr (S::QUADK) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t a = key_addr<2 * KB, S::LOGSK>(bf.k[t], (8 * j + 2 * u) * KB, lutk_lane, kmask);
-          ah[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + a);
-          al[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
+          for (int u = 0; u < 2; ++u) {
+            const uint32_t a = key_addr<4 * KB, S::LOGSK>(bf.k[t], (8 * j + 4 * u) * KB, lutk_lane, kmask);
+            const uint2 eh = lds_at<uint2>(lds, S::LUTK_OFF + a);
+            const uint2 el = lds_at<uint2>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
+            ah[2 * u] = eh.x, ah[2 * u + 1] = eh.y;
+            al[2 * u] = el.x, al[2 * u + 1] = el.y;
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint32_t a = key_addr<2 * KB, S::LOGSK>(bf.k[t], (8 * j + 2 * u) * KB, lutk_lane, kmask);
+            ah[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + a);
+            al[u] = lds_at<uint32_t>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
+          }
         }
         Ch[t] = mfma_f16(ah, qbh[j], Ch[t]);
         Cl[t] = mfma_f16(al, qbh[j], Cl[t]);
@@ -396,36 +469,66 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
 
   auto finish = [&](const Buf& bf, const Scores& C, int s0) {
     // ---- value operands first (independent of the softmax)
-    constexpr uint32_t MEVEN = [] {
-      uint32_t m = 0;
-      for (int j = 0; j < CPL; j += 2) m |= ((1u << VB) - 1u) << (j * VB);
-      return m;
-    }();
-    uint32_t zl[4], zh[4];
+    constexpr int NVR = S::SIGNV ? 2 : 4;  // value-table reads per coordinate
+    uint2 vop[CPL][NVR];
+    if constexpr (S::SIGNV) {
+      // nibble keys of 4 tokens (bit e: token e of a tile) for one coordinate:
+      // first interleave token pairs (even coordinates in zl, odd in zh), then
+      // pairs of pairs; zq[t][q] holds two keys (nibbles 0 and 1) for the
+      // coordinates q = 0: 0, 4;  1: 2, 6;  2: 1, 5;  3: 3, 7
+      static_assert(CPL == 8, "one byte of one-bit fields per token and lane");
+      uint32_t zq[2][4];
 #pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      uint32_t xa, xb;
-      if constexpr (VRAW == 2) {
-        xa = __builtin_amdgcn_alignbit(bf.v[2 * e2][1], bf.v[2 * e2][0], vsh);
-        xb = __builtin_amdgcn_alignbit(bf.v[2 * e2 + 1][1], bf.v[2 * e2 + 1][0], vsh);
-      } else if constexpr (S::SEGBITS < 32) {
-        xa = bf.v[2 * e2][0] >> vsh;
-        xb = bf.v[2 * e2 + 1][0] >> vsh;
-      } else {
-        xa = bf.v[2 * e2][0];
-        xb = bf.v[2 * e2 + 1][0];
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t x0 = bf.v[4 * t][0], x1 = bf.v[4 * t + 1][0];
+        const uint32_t x2 = bf.v[4 * t + 2][0], x3 = bf.v[4 * t + 3][0];
+        const uint32_t zl01 = (x0 & 0x55u) | ((x1 << 1) & ~0x55u);
+        const uint32_t zh01 = ((x0 >> 1) & 0x55u) | (x1 & ~0x55u);
+        const uint32_t zl23 = (x2 & 0x55u) | ((x3 << 1) & ~0x55u);
+        const uint32_t zh23 = ((x2 >> 1) & 0x55u) | (x3 & ~0x55u);
+        zq[t][0] = (zl01 & 0x33u) | ((zl23 << 2) & ~0x33u);
+        zq[t][1] = ((zl01 >> 2) & 0x33u) | (zl23 & ~0x33u);
+        zq[t][2] = (zh01 & 0x33u) | ((zh23 << 2) & ~0x33u);
+        zq[t][3] = ((zh01 >> 2) & 0x33u) | (zh23 & ~0x33u);
       }
-      zl[e2] = (xa & MEVEN) | ((xb << VB) & ~MEVEN);
-      zh[e2] = ((xa >> VB) & MEVEN) | (xb & ~MEVEN);
-    }
-    uint2 vop[CPL][4];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c)
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint32_t z[1] = {zq[t][2 * (c & 1) + ((c >> 1) & 1)]};
+          vop[c][t] = lds_at<uint2>(lds, VOFF + key_addr<4, S::LOGSV>(z, 4 * (c >> 2), lutv_lane, vmask));
+        }
+    } else {
+      constexpr uint32_t MEVEN = [] {
+        uint32_t m = 0;
+        for (int j = 0; j < CPL; j += 2) m |= ((1u << VB) - 1u) << (j * VB);
+        return m;
+      }();
+      uint32_t zl[4], zh[4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const uint32_t z[1] = {(c & 1) ? zh[e2] : zl[e2]};
-        vop[c][e2] = lds_at<uint2>(lds, S::LUTV_OFF + key_addr<2 * VB, S::LOGSV>(z, (c >> 1) * 2 * VB, lutv_lane, vmask));
+        uint32_t xa, xb;
+        if constexpr (VRAW == 2) {
+          xa = __builtin_amdgcn_alignbit(bf.v[2 * e2][1], bf.v[2 * e2][0], vsh);
+          xb = __builtin_amdgcn_alignbit(bf.v[2 * e2 + 1][1], bf.v[2 * e2 + 1][0], vsh);
+        } else if constexpr (S::SEGBITS < 32) {
+          xa = bf.v[2 * e2][0] >> vsh;
+          xb = bf.v[2 * e2 + 1][0] >> vsh;
+        } else {
+          xa = bf.v[2 * e2][0];
+          xb = bf.v[2 * e2 + 1][0];
+        }
+        zl[e2] = (xa & MEVEN) | ((xb << VB) & ~MEVEN);
+        zh[e2] = ((xa >> VB) & MEVEN) | (xb & ~MEVEN);
       }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const uint32_t z[1] = {(c & 1) ? zh[e2] : zl[e2]};
+          vop[c][e2] = lds_at<uint2>(lds, VOFF + key_addr<2 * VB, S::LOGSV>(z, (c >> 1) * 2 * VB, lutv_lane, vmask));
+        }
+    }
     float nk[8], nv[8], sc[8], d[8];
     {
       float a0[4], a1[4], c0[4], c1[4];
@@ -504,6 +607,10 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
       for (int c = 0; c < CPL; ++c)
 #pragma unroll
         for (int i = 0; i < 4; ++i) O[c][i] *= fr[i];
+      if constexpr (S::SIGNV) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Lw[i] *= fr[i];
+      }
       m_row = mn;
       E = e2;
       vsc = ldexpf(1.f, -E);
@@ -526,12 +633,23 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     const uint32_t w23 = pack_f16x2(w[2], w[3]);
     const uint32_t x01 = pack_f16x2(w[4], w[5]);
     const uint32_t x23 = pack_f16x2(w[6], w[7]);
-    const u32x4_t A0 = {w01, w01, w23, w23};
-    const u32x4_t A1 = {x01, x01, x23, x23};
+    if constexpr (S::SIGNV) {
+      // k slots: the lane's 8 tokens (tile 0's four, then tile 1's) against
+      // their signs; the weight sums ride along when the codebook's midpoint
+      // is not zero
+      const u32x4_t A = {w01, w23, x01, x23};
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      O[c] = mfma_f16(A0, u32x4_t{vop[c][0].x, vop[c][0].y, vop[c][1].x, vop[c][1].y}, O[c]);
-      O[c] = mfma_f16(A1, u32x4_t{vop[c][2].x, vop[c][2].y, vop[c][3].x, vop[c][3].y}, O[c]);
+      for (int c = 0; c < CPL; ++c)
+        O[c] = mfma_f16(A, u32x4_t{vop[c][0].x, vop[c][0].y, vop[c][1].x, vop[c][1].y}, O[c]);
+      if (v_mid != 0.f) Lw = mfma_f16(A, u32x4_t{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u}, Lw);
+    } else {
+      const u32x4_t A0 = {w01, w01, w23, w23};
+      const u32x4_t A1 = {x01, x01, x23, x23};
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        O[c] = mfma_f16(A0, u32x4_t{vop[c][0].x, vop[c][0].y, vop[c][1].x, vop[c][1].y}, O[c]);
+        O[c] = mfma_f16(A1, u32x4_t{vop[c][2].x, vop[c][2].y, vop[c][3].x, vop[c][3].y}, O[c]);
+      }
     }
   };
 
@@ -577,6 +695,11 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     s_wl[wave * NQ + n] = lr;
     s_we[wave * NQ + n] = ldexpf(1.f, E);  // undoes the weights' 2^-E
   }
+  float* s_wv = reinterpret_cast<float*>(lds + S::WV_OFF);
+  if (S::SIGNV && n == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_wv[wave * NQ + 4 * g + i] = Lw[i];
+  }
   lds_barrier();
   float* s_fo = reinterpret_cast<float*>(lds + S::FO_OFF);
   float* s_fl = reinterpret_cast<float*>(lds + S::FL_OFF);
@@ -585,17 +708,21 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w * NQ + r]);
-    float lt = 0.f;
-    const float oscale = __builtin_amdgcn_rcpf(cbs_v);  // a power of two: exact
+    float lt = 0.f, lv = 0.f;
+    // table values carry the factor cbs_v (a power of two: exact); signs v_half
+    const float oscale = S::SIGNV ? v_half : __builtin_amdgcn_rcpf(cbs_v);
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float wm = s_wm[w * NQ + r];
       const float f = wm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm - M);
       lt = fmaf(s_wl[w * NQ + r], f, lt);
-      s_wf[w * NQ + r] = f * s_we[w * NQ + r] * oscale;
+      const float fe = f * s_we[w * NQ + r];
+      s_wf[w * NQ + r] = fe * oscale;
+      if (S::SIGNV) lv = fmaf(s_wv[w * NQ + r], fe, lv);
     }
     s_fl[r] = lt;
     s_fl[NQ + r] = M;
+    s_fl[2 * NQ + r] = S::SIGNV ? v_mid * lv : 0.f;
   }
   lds_barrier();
   for (int idx = tid; idx < NQ * D; idx += NT) {
@@ -603,7 +730,7 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     float a = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) a = fmaf(s_wo[(w * NQ) * D + idx], s_wf[w * NQ + r], a);
-    s_fo[idx] = a;
+    s_fo[idx] = S::SIGNV ? a + s_fl[2 * NQ + r] : a;
   }
   lds_barrier();
 

@@ -114,18 +114,25 @@ def build_case(seed, B, Hq, Hkv, L, T, d, kb, vb, rot="hadamard", qdt="bf16", no
 
 
 def run_case(device, seed, B, Hq, Hkv, L, T, d, kb, vb, rot="hadamard", qdt="bf16", causal=None,
-             lengths=None, norm="float32", starts=None):
+             lengths=None, norm="float32", starts=None, v_codebook=None):
+    """v_codebook: value levels to attend with in place of the Beta codebook
+    (the cache's indices are drawn with the Beta codebook either way)."""
     causal = (L > 1) if causal is None else causal
     q, kp, kn, vp, vn, kr, vr = build_case(seed, B, Hq, Hkv, L, T, d, kb, vb, rot, qdt, norm)
+    vcb = O.beta_codebook(d, vb) if v_codebook is None else np.asarray(v_codebook, np.float32)
     want = O.attention(q, kp, kn, vp, vn, k_bits=kb, v_bits=vb, k_codebook=O.beta_codebook(d, kb),
-                       v_codebook=O.beta_codebook(d, vb), rot_kind=rot, k_rot=kr, v_rot=vr,
+                       v_codebook=vcb, rot_kind=rot, k_rot=kr, v_rot=vr,
                        scale=1 / math.sqrt(d), q_dtype=qdt, causal=causal, lengths=lengths,
                        starts=starts)
     nd = torch.float16 if norm == "float16" else torch.float32
     kn_t, ki, vn_t, vi = to_buffers(kp, kn, vp, vn, device, norm_dtype=nd)
     sl = torch.tensor(lengths, dtype=torch.int32, device=device) if lengths is not None else None
+    vcodec = ops.Codec(d, vb, 1, rot)
+    if v_codebook is not None:
+        vcodec.codebook = vcb
+        vcodec.midpoints = O.midpoints(vcb)
     out = ops.attention_packed(q_tensor(q, qdt, device), kn_t, ki, vn_t, vi,
-                               ops.Codec(d, kb, 0, rot), ops.Codec(d, vb, 1, rot),
+                               ops.Codec(d, kb, 0, rot), vcodec,
                                1 / math.sqrt(d), causal, seq_lens=sl,
                                seq_starts=None if starts is None else torch.tensor(starts))
     label = f"B{B} Hq{Hq} Hkv{Hkv} L{L} T{T} d{d} k{kb}v{vb} {rot} {qdt}"
@@ -232,6 +239,7 @@ def test_split_with_fully_masked_rows(device, d):
     (32, 8, 4, 3, 2, [5000, 3, 777]),  # ragged, one sequence shorter than the drafts
     (4, 1, 40, 3, 3, None),            # 160 rows: ten row groups (a prefill chunk)
     (24, 8, 4, 2, 2, [1, 4100]),       # 12 rows, ragged with a one-token sequence
+    (16, 4, 4, 1, 1, [4999, 2600]),    # 1-bit keys and values, ragged
 ])
 def test_rows16_groups(device, Hq, Hkv, L, kb, vb, lengths):
     """16-row groups at d = 128 (verify, wide GQA, prefill chunks)."""
@@ -241,8 +249,23 @@ def test_rows16_groups(device, Hq, Hkv, L, kb, vb, lengths):
 
 
 @pytest.mark.parametrize("qdt", ["f32", "f16"])
-def test_rows16_query_dtypes_and_f16_norms(device, qdt):
-    run_case(device, 6, 2, 32, 8, 2, 1300, 128, 3, 3, qdt=qdt, norm="float16")
+@pytest.mark.parametrize("kb,vb", [(3, 3), (2, 1)])
+def test_rows16_query_dtypes_and_f16_norms(device, qdt, kb, vb):
+    run_case(device, 6, 2, 32, 8, 2, 1300, 128, kb, vb, qdt=qdt, norm="float16")
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,kb,vb,T", [
+    (32, 8, 4, 2, 1, 5000),   # 16-row groups (verify)
+    (32, 8, 4, 1, 1, 777),    # 16-row groups, one split
+    (8, 2, 1, 2, 1, 3000),    # <= 4 rows per kv head (decode)
+    (8, 1, 16, 3, 1, 2100),   # 128 rows: prefill tiles
+])
+def test_asymmetric_one_bit_value_codebook(device, Hq, Hkv, L, kb, vb, T):
+    """A 1-bit value codebook whose levels are not symmetric about zero: the
+    16-row kernel forms v = mid + half * s with s = +-1, so the midpoint term
+    (the sum of the weights) must be carried; the other kernels read the
+    levels directly."""
+    run_case(device, 70 + L + kb, 1, Hq, Hkv, L, T, 128, kb, vb, v_codebook=[-0.031, 0.094])
 
 
 def test_rows16_split_with_fully_masked_rows(device):
