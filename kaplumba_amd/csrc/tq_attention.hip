@@ -370,9 +370,10 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   p.rscale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)));
-  // the staged row-group kernel leaves Hadamard partials in the rotated basis
+  // the staged row-group kernel and the 16-row kernel leave Hadamard
+  // partials in the rotated basis
   p.merge_rot = (kv_kind == TQ_KV_PACKED && !prod && rot_kind == TQ_ROT_HADAMARD &&
-                 small_rows_path(kv_kind, dim, (Hq / Hkv) * L))
+                 (small_rows_path(kv_kind, dim, (Hq / Hkv) * L) || rows16_path(kv_kind, dim, (Hq / Hkv) * L)))
                     ? 1
                     : 0;
   int rc = TQ_OK;
@@ -411,13 +412,21 @@ int attention_impl(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, in
   // one workgroup per query row; for the dense rotation one per 64 output
   // columns of a row group (R_V^-1 is read once per row group)
   if (p.merge_rot) {
-    // the staged row-group kernel: 4-row groups, partials in the rotated basis
-    const dim3 rgrid(4, static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+    // partials in the rotated basis: 4-row groups (staged kernel) or 16-row
+    // groups (d = 128)
     const int valid = (seq_starts || seq_lens) ? -1 : static_cast<int>((T + sp.chunk - 1) / sp.chunk);
-    switch (dim) {
-      case 64: hipLaunchKernelGGL(attn_merge_rot_kernel<64>, rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, Hkv, p); break;
-      default: hipLaunchKernelGGL(attn_merge_rot_kernel<128>, rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot, sp.n_splits, valid, Hkv, p); break;
-    }
+    const dim3 rgrid(static_cast<unsigned>(sp.nq), static_cast<unsigned>(Hkv * sp.n_rg), static_cast<unsigned>(B));
+    if (sp.nq == 16 && dim == 128)
+      hipLaunchKernelGGL((attn_merge_rot_kernel<128, 16>), rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot,
+                         sp.n_splits, valid, Hkv, sp.n_rg, p);
+    else if (sp.nq == 4 && dim == 64)
+      hipLaunchKernelGGL((attn_merge_rot_kernel<64, 4>), rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot,
+                         sp.n_splits, valid, Hkv, sp.n_rg, p);
+    else if (sp.nq == 4 && dim == 128)
+      hipLaunchKernelGGL((attn_merge_rot_kernel<128, 4>), rgrid, dim3(kWave), 0, st, p.po, p.pml, p.vrot,
+                         sp.n_splits, valid, Hkv, sp.n_rg, p);
+    else
+      return fail(TQ_ERR_UNSUPPORTED, "attention: no rotated-basis merge for %d-row groups at dim %d", sp.nq, dim);
     return check_launch("attn_merge_rot_kernel");
   }
   const unsigned mx = rot_kind == TQ_ROT_DENSE ? static_cast<unsigned>(dim / 64) : static_cast<unsigned>(sp.nq);

@@ -20,15 +20,19 @@
 //         below 2^-22 relative).
 //     Output: lane (g, row n), register i = token 4g + i of the tile.
 //   softmax per lane: 8 tokens of row n (4 per tile).
+//     With 1- and 2-bit keys one table read gives four coordinates (an
+//     8-byte hi entry and an 8-byte lo entry, 32 replicas: conflict-free).
 //   values  O[row][d] = sum_tok w[row][tok] * v[tok][d]   (16 x 16 tiles)
 //     A = weights: lane (row n, g) holds tokens 4g .. 4g+3 and 16+4g ..
 //         16+4g+3 as f16 -- exactly its own 8 weights: no transpose,
 //     B = values: as in the small kernel, (hi pair, lo pair) of two tokens
-//         per 8-byte table read against weights (w_a, w_b, w_a, w_b).
+//         per 8-byte table read against weights (w_a, w_b, w_a, w_b);
+//         1-bit values as v = mid + half * s: the signs s = +-1 of four
+//         tokens per 8-byte read, exact in f16, all 32 tokens in one MFMA.
 //     Output: lane (g, n), register i = row 4g + i, coordinate (D/16) n + c.
-// Softmax, value-norm exponent, table replication and the split protocol
-// are those of the small kernel; the partials use the row-group layout of
-// attn_merge_kernel (16 rows per group).
+// Softmax, value-norm exponent and table replication are those of the small
+// kernel.  Splits leave o in the rotated basis for the merge (16 rows per
+// group): attn_merge_rot_kernel applies R_V^-1 once per row.
 // Semantics: quantized_attention, turboquant_cache.py:5110-5203.
 #pragma once
 
@@ -58,7 +62,10 @@ struct Rows16Shape {
   static constexpr int KCO = QUADK ? 4 : 2;
   static constexpr int KEB = 2 * KCO;  // bytes per hi or lo entry
   static constexpr int KKEYS = 1 << (KCO * KB);
-  static constexpr int REPK = QUADK ? (KKEYS <= 16 ? 32 : 16) : (KKEYS <= 64 ? 64 : 16);
+  // 32 replicas of 8-byte entries: the 32 lanes of one half-wave read
+  // distinct banks whatever their keys (16 where the LDS cannot hold 2 x 64
+  // KiB of key tables beside wide value tables)
+  static constexpr int REPK = QUADK ? (KKEYS <= 16 || VB <= 2 ? 32 : 16) : (KKEYS <= 64 ? 64 : 16);
   static constexpr int LOGSK = ilog2(REPK * KEB);
   // values: a lane holds CPL consecutive coordinates of 8 tokens
   static constexpr int CPL = D / 16;
@@ -100,7 +107,10 @@ struct Rows16Shape {
   static_assert(KW * 32 == QTR * KB, "key quarter rows are whole words");
   static_assert(SEGBITS <= 32, "value segment in one word");
   static_assert(BYTES <= 160 * 1024, "LDS per workgroup");
-  static_assert(LUTK_OFF + KTAB < 65536, "key tables fit the instruction offset field");
+  // the lo table sits at an instruction offset when that fits, else its
+  // offset (a power of two above every hi-table address) is ORed in
+  static constexpr bool KLO_IN_BASE = LUTK_OFF + KTAB > 65535;
+  static_assert(!KLO_IN_BASE || (LUTK_OFF == 0 && (KTAB & (KTAB - 1)) == 0), "lo table offset ORs into the address");
   static_assert(!VOFF_IN_BASE || LUTV_OFF % VTAB == 0, "value table offset ORs into the lane base");
 };
 
@@ -283,7 +293,7 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   for (int i = 0; i < (1 << VB); ++i) vmax = fmaxf(vmax, fabsf(cvb[i]));
   const float sk = f16_split_scale(kmax);
   const float cbs_v = f16_split_scale(vmax);
-  static_assert(S::KKEYS * S::REPK / 8 <= NT && S::VKEYS * S::REPV / 8 <= NT, "one table slot per thread");
+  static_assert((S::QUADK || S::KKEYS * S::REPK / 8 <= NT) && S::VKEYS * S::REPV / 8 <= NT, "one table slot per thread");
   // a thread writes 8 consecutive replicas of one key
   {
     const int kslot = tid < S::KKEYS * S::REPK / 8 ? tid : 0;
@@ -291,14 +301,16 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     const int kkey = kslot / (S::REPK / 8), vkey = vslot / (S::REPV / 8);
     if constexpr (S::QUADK) {
       // key f0 | f1 << KB | f2 << 2 KB | f3 << 3 KB: f16 parts of c[f0] s .. c[f3] s
-      uint32_t h[4], l[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) split_f16(mux_pick<KB>(ckb, (kkey >> (KB * i)) & ((1 << KB) - 1)) * sk, h[i], l[i]);
-      if (tid < S::KKEYS * S::REPK / 8) {
+      for (int t = tid; t < S::KKEYS * S::REPK / 8; t += NT) {
+        const int key = t / (S::REPK / 8);
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) split_f16(mux_pick<KB>(ckb, (key >> (KB * i)) & ((1 << KB) - 1)) * sk, h[i], l[i]);
         const uint32_t h01 = h[0] | (h[1] << 16), h23 = h[2] | (h[3] << 16);
         const uint32_t l01 = l[0] | (l[1] << 16), l23 = l[2] | (l[3] << 16);
-        uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + kslot * 4;
-        uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + kslot * 4;
+        uint4* dh = reinterpret_cast<uint4*>(lds + S::LUTK_OFF) + t * 4;
+        uint4* dl = reinterpret_cast<uint4*>(lds + S::LUTK_OFF + S::KTAB) + t * 4;
         dh[0] = dh[1] = dh[2] = dh[3] = make_uint4(h01, h23, h01, h23);
         dl[0] = dl[1] = dl[2] = dl[3] = make_uint4(l01, l23, l01, l23);
       }
@@ -421,9 +433,12 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   for (int c = 0; c < CPL; ++c) O[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_row = -INFINITY;  // reference max of row n (log2 units)
   int E = -1000;            // value-norm exponent of the wave (max ||v|| <= 2^E when set)
-  float vsc = 0.f;          // 2^-E
+  // The weights are p 2^-E ||v||: 2^-E rides in the exponent, p 2^-E =
+  // exp2(s - (m_row + E)), so l and O both count in units of 2^E.
+  float mE = -INFINITY;     // m_row + E
+  float d_lim = 0.f;        // kLazy - E: the lazy bound on s - mE
   float nv_lim = 0.f;       // 2^(E + 8): larger norms could overflow an f16 weight
-  float l_acc = 0.f;        // sum of p over this lane's tokens of row n
+  float l_acc = 0.f;        // sum of p 2^-E over this lane's tokens of row n
   // 1-bit values: v = v_mid + v_half s.  Lw accumulates the f16 weights
   // (row 4g + i in register i, every column alike) when v_mid != 0.
   f32x4_t Lw = {0.f, 0.f, 0.f, 0.f};
@@ -448,7 +463,8 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
           for (int u = 0; u < 2; ++u) {
             const uint32_t a = key_addr<4 * KB, S::LOGSK>(bf.k[t], (8 * j + 4 * u) * KB, lutk_lane, kmask);
             const uint2 eh = lds_at<uint2>(lds, S::LUTK_OFF + a);
-            const uint2 el = lds_at<uint2>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
+            const uint2 el = S::KLO_IN_BASE ? lds_at<uint2>(lds, opaque(a) | S::KTAB)
+                                            : lds_at<uint2>(lds, S::LUTK_OFF + S::KTAB + opaque(a));
             ah[2 * u] = eh.x, ah[2 * u + 1] = eh.y;
             al[2 * u] = el.x, al[2 * u + 1] = el.y;
           }
@@ -547,7 +563,7 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       sc[k] = own_reg(C.c[k >> 2][k & 3]);
-      d[k] = fmaf(sc[k], nk[k] * kscale, -m_row);
+      d[k] = fmaf(sc[k], nk[k] * kscale, -mE);
     }
     float dmax = d[0], nvmax = nv[0];
 #pragma unroll
@@ -556,7 +572,7 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
       nvmax = fmaxf(nvmax, nv[k]);
     }
     const bool edge = s0 + SUB > t_end || s0 + SUB - 1 > lim_min;  // wave-uniform
-    if (edge || __any((dmax > kLazy || nvmax > nv_lim) ? 1 : 0)) {
+    if (edge || __any((dmax > d_lim || nvmax > nv_lim) ? 1 : 0)) {
       // ---- slow path: masks, new reference max / norm exponent, rescale
       if (odd_tail && edge) {
 #pragma unroll
@@ -591,11 +607,11 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
       frexpf(vm, &ev);
       const int e2 = ev > E ? ev : E;
       const float mn = (rm > m_row + kLazy || m_row == -INFINITY) ? fmaxf(m_row, rm) : m_row;
-      // l scales by 2^(m_old - m_new), O also by 2^(E_old - E_new); both
-      // start at zero (the first sub-chunk has m_old = -inf)
+      // l and O scale by 2^(m_old - m_new) 2^(E_old - E_new); both start at
+      // zero (the first sub-chunk has m_old = -inf)
       const float am = (m_row == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_row - mn);
       const float ao = am * ldexpf(1.f, E - e2);
-      l_acc *= am;
+      l_acc *= ao;
       // O register i of lane group g' is row 4 g' + i: its factor sits in lane 4 g' + i
       float ar[NQ];
 #pragma unroll
@@ -613,19 +629,21 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
       }
       m_row = mn;
       E = e2;
-      vsc = ldexpf(1.f, -E);
+      mE = m_row + static_cast<float>(E);
+      d_lim = kLazy - static_cast<float>(E);
       nv_lim = ldexpf(1.f, E + 8);
-      // masked keys (-FLT_MAX) get weight 1 when their whole row is masked
-      // (m = -FLT_MAX), else 0; keys past the end (-inf) always 0
+      // masked keys (-FLT_MAX) get weight 2^-E when their whole row is masked
+      // (m = -FLT_MAX; s - m first, so that the exponent is exact), else 0;
+      // keys past the end (-inf) always 0
 #pragma unroll
-      for (int k = 0; k < 8; ++k) d[k] = sc[k] - m_row;
+      for (int k = 0; k < 8; ++k) d[k] = (sc[k] - m_row) - static_cast<float>(E);
     }
     float w[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float pe = __builtin_amdgcn_exp2f(d[k]);
+      const float pe = __builtin_amdgcn_exp2f(d[k]);  // p 2^-E
       l_acc += pe;
-      w[k] = pe * (nv[k] * vsc);
+      w[k] = pe * nv[k];
     }
     // ---- weights to the A operands: tile 0's four tokens, then tile 1's;
     // each pair twice, against the (hi pair, lo pair) k slots of the values
@@ -693,7 +711,7 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     // a wave without tokens keeps m = -inf and contributes nothing
     s_wm[wave * NQ + n] = m_row;
     s_wl[wave * NQ + n] = lr;
-    s_we[wave * NQ + n] = ldexpf(1.f, E);  // undoes the weights' 2^-E
+    s_we[wave * NQ + n] = ldexpf(1.f, E);  // undoes the 2^-E of l and O
   }
   float* s_wv = reinterpret_cast<float*>(lds + S::WV_OFF);
   if (S::SIGNV && n == 0) {
@@ -715,8 +733,8 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     for (int w = 0; w < NW; ++w) {
       const float wm = s_wm[w * NQ + r];
       const float f = wm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm - M);
-      lt = fmaf(s_wl[w * NQ + r], f, lt);
       const float fe = f * s_we[w * NQ + r];
+      lt = fmaf(s_wl[w * NQ + r], fe, lt);
       s_wf[w * NQ + r] = fe * oscale;
       if (S::SIGNV) lv = fmaf(s_wv[w * NQ + r], fe, lv);
     }
@@ -735,21 +753,10 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
   lds_barrier();
 
   if (nvalid > 1) {
-    // this split's partial for attn_merge_kernel: o through R_V^-1 (Hadamard),
-    // then o[r][:] and (m, l) per row with m in natural-log units
-    if (!dense) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int r = wave + NW * h;
-        float y[QE];
-#pragma unroll
-        for (int e = 0; e < QE; ++e) y[e] = s_fo[r * D + lane + e * kWave];
-        wave_fwht<D>(y, lsg);
-#pragma unroll
-        for (int e = 0; e < QE; ++e) s_fo[r * D + lane + e * kWave] = y[e] * p.rscale * p.vrot[lane + e * kWave];
-      }
-    }
-    lds_barrier();
+    // this split's partial: o[r][:] still in the rotated basis (the merge
+    // applies R_V^-1 once per row: attn_merge_rot_kernel for the Hadamard
+    // rotation, attn_merge_kernel for the dense one), and (m, l) per row
+    // with m in natural-log units
     const int64_t grp = (static_cast<int64_t>(b) * p.Hkv + gk) * p.n_rg + rg;
     float4* po4 = reinterpret_cast<float4*>(p.po + (grp * p.n_splits + split) * static_cast<int64_t>(NQ) * D);
     for (int idx = tid; idx < NQ * D / 4; idx += NT) po4[idx] = reinterpret_cast<const float4*>(s_fo)[idx];

@@ -175,13 +175,16 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p)
   }
 }
 
-// Merge of the staged row-group kernel's splits (tq_attn_stage.h): 4-row
-// groups, Hadamard partials still in the rotated basis.  The hot arguments
-// (partial buffers, split counts, R_V's signs, kv heads) come first and are preloaded
-// into SGPRs, so the partial loads go out without waiting for the argument
-// segment; valid = the split count of a sequence when no per-sequence
-// windows exist (-1: from seq_window).  Workgroup = one wave = one query row
-// of one (sequence, kv head); lane l owns coordinates l + 64 e.  Lane u
+// Merge of the splits of the staged row-group kernel (tq_attn_stage.h, NQ =
+// 4 rows per group) and of the 16-row kernel (tq_attn_rows16.h, NQ = 16, n_rg
+// groups per kv head): Hadamard partials still in the rotated basis.  The hot
+// arguments (partial buffers, split counts, R_V's signs, kv heads, row
+// groups) come first and are preloaded into SGPRs, so the partial loads go
+// out without waiting for the argument segment; valid = the split count of a
+// sequence when no per-sequence windows exist (-1: from seq_window).
+// Workgroup = one wave = one query row of one (sequence, kv head, row
+// group); grid (NQ, kv heads x row groups, batch); lane l owns coordinates
+// l + 64 e.  Lane u
 // loads split u's (m, l) and every lane its o values of the MB splits, all
 // loads in flight at once; the log-sum-exp weights come from wave
 // reductions and reach every lane by readlane, so the fold needs no LDS and
@@ -189,16 +192,16 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnParams p)
 // Walsh-Hadamard transform; the row is stored in the query dtype.
 constexpr int kMergeRotSplits = 32;  // splits per round trip of attn_merge_rot_kernel
 
-template <int D>
+template <int D, int NQ>
 __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, const float* pml,
                                                                const float* vrot, int n_splits,
-                                                               int valid, int hkv, AttnParams p) {
-  constexpr int NQ = 4;
+                                                               int valid, int hkv, int n_rg, AttnParams p) {
   constexpr int QE = D / kWave;
   constexpr int MB = kMergeRotSplits;
   const int lane = threadIdx.x;
   const int j = blockIdx.x;
-  const int gk = blockIdx.y;
+  const int gk = static_cast<int>(blockIdx.y) / n_rg;
+  const int rg = static_cast<int>(blockIdx.y) % n_rg;
   const int b = blockIdx.z;
   MERGE_STAMP(0);
   const int nvalid = valid >= 0 ? valid : [&] {
@@ -206,7 +209,8 @@ __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, 
     return win.len > 0 ? static_cast<int>((win.len + p.chunk - 1) / p.chunk) : 0;
   }();
   if (nvalid <= 1) return;  // the partial kernel wrote these rows itself
-  const int64_t grp = static_cast<int64_t>(b) * hkv + gk;  // (hkv preloaded: no wait for the grid size)
+  // (hkv and n_rg preloaded: no wait for the grid size or the argument segment)
+  const int64_t grp = static_cast<int64_t>(b) * hkv * n_rg + blockIdx.y;
   const float* po_g = po + grp * static_cast<int64_t>(n_splits) * NQ * D;
   const float2* pml_g = reinterpret_cast<const float2*>(pml) + grp * static_cast<int64_t>(n_splits) * NQ;
   // R_V^-1's signs, loaded with the partials
@@ -255,8 +259,9 @@ __global__ __launch_bounds__(kWave) void attn_merge_rot_kernel(const float* po, 
   wave_fwht<D>(y, sg6);
   // (rows past the group's last exist in the partials but not in the output;
   // checked only here, so the partial loads above go out first)
-  if (j >= p.R * p.L) return;
-  const int64_t qo = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + j / p.L) * p.L + j % p.L) * D;
+  const int jr = rg * NQ + j;  // row of the kv head's GQA group
+  if (jr >= p.R * p.L) return;
+  const int64_t qo = ((static_cast<int64_t>(b) * p.Hq + gk * p.R + jr / p.L) * p.L + jr % p.L) * D;
 #pragma unroll
   for (int e = 0; e < QE; ++e) store_out(p.out, p.q_dtype, qo + lane + e * kWave, y[e] * p.rscale * vr[e]);
   MERGE_STAMP(3);
