@@ -216,12 +216,13 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
       }
     }
     if constexpr (S::SIGNV) {
-      // the lane's CPL = 8 one-bit fields of each token are byte n of the row
-      const uint32_t vo = t0 * (PWV * 4) + n;
+      // the lane's CPL = 8 one-bit fields of each token are byte n of the
+      // row; tokens 4g + e and 16 + 4g + e at constant offsets from one base
+      const uint32_t vo = (t0 + 4 * g) * (PWV * 4) + n;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int tok = (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
-        bf.v[e][0] = __builtin_amdgcn_raw_buffer_load_b8(vrs, vo + tok * (PWV * 4), 0, 0);
+        const uint32_t dt = e < 4 ? e : 16 + (e - 4);
+        bf.v[e][0] = __builtin_amdgcn_raw_buffer_load_b8(vrs, vo + dt * (PWV * 4), 0, 0);
       }
     } else {
       const uint32_t vo = t0 * (PWV * 4) + v_lane;
@@ -488,31 +489,29 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
     constexpr int NVR = S::SIGNV ? 2 : 4;  // value-table reads per coordinate
     uint2 vop[CPL][NVR];
     if constexpr (S::SIGNV) {
-      // nibble keys of 4 tokens (bit e: token e of a tile) for one coordinate:
-      // first interleave token pairs (even coordinates in zl, odd in zh), then
-      // pairs of pairs; zq[t][q] holds two keys (nibbles 0 and 1) for the
-      // coordinates q = 0: 0, 4;  1: 2, 6;  2: 1, 5;  3: 3, 7
+      // nibble keys of 4 tokens (bit e: token e of a tile) for one coordinate.
+      // The tile's four bytes (token e = byte e, coordinate c = bit c) form
+      // a 4 x 8 bit matrix; two delta swaps transpose its 4 x 4 blocks, after
+      // which the nibble at bit 8 (c & 3) + 4 (c >> 2) holds coordinate c's
+      // four tokens.
       static_assert(CPL == 8, "one byte of one-bit fields per token and lane");
-      uint32_t zq[2][4];
+      uint32_t y[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint32_t x0 = bf.v[4 * t][0], x1 = bf.v[4 * t + 1][0];
-        const uint32_t x2 = bf.v[4 * t + 2][0], x3 = bf.v[4 * t + 3][0];
-        const uint32_t zl01 = (x0 & 0x55u) | ((x1 << 1) & ~0x55u);
-        const uint32_t zh01 = ((x0 >> 1) & 0x55u) | (x1 & ~0x55u);
-        const uint32_t zl23 = (x2 & 0x55u) | ((x3 << 1) & ~0x55u);
-        const uint32_t zh23 = ((x2 >> 1) & 0x55u) | (x3 & ~0x55u);
-        zq[t][0] = (zl01 & 0x33u) | ((zl23 << 2) & ~0x33u);
-        zq[t][1] = ((zl01 >> 2) & 0x33u) | (zl23 & ~0x33u);
-        zq[t][2] = (zh01 & 0x33u) | ((zh23 << 2) & ~0x33u);
-        zq[t][3] = ((zh01 >> 2) & 0x33u) | (zh23 & ~0x33u);
+        uint32_t x = bf.v[4 * t][0] | (bf.v[4 * t + 1][0] << 8) | (bf.v[4 * t + 2][0] << 16) |
+                     (bf.v[4 * t + 3][0] << 24);
+        uint32_t u = ((x >> 7) ^ x) & 0x00aa00aau;  // 2 x 2 blocks
+        x ^= u ^ (u << 7);
+        u = ((x >> 14) ^ x) & 0x0000ccccu;  // 4 x 4 blocks of them
+        x ^= u ^ (u << 14);
+        y[t] = x;
       }
 #pragma unroll
       for (int c = 0; c < CPL; ++c)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const uint32_t z[1] = {zq[t][2 * (c & 1) + ((c >> 1) & 1)]};
-          vop[c][t] = lds_at<uint2>(lds, VOFF + key_addr<4, S::LOGSV>(z, 4 * (c >> 2), lutv_lane, vmask));
+          const uint32_t z[1] = {y[t]};
+          vop[c][t] = lds_at<uint2>(lds, VOFF + key_addr<4, S::LOGSV>(z, 8 * (c & 3) + 4 * (c >> 2), lutv_lane, vmask));
         }
     } else {
       constexpr uint32_t MEVEN = [] {
