@@ -459,7 +459,22 @@ __global__ __launch_bounds__(512, 1) void attn_rows16_kernel(AttnParams p) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         u32x4_t ah, al;
-        if constexpr (S::QUADK) {
+        if constexpr (S::QUADK && KB == 2 && S::REPK == 32) {
+          // the 8-bit key is byte k of a key word: v_perm_b32 puts it into
+          // address byte 1 (entries of one key span 256 B) beside the lane's
+          // replica offset (byte 0) and the lo table's offset (byte 2)
+          static_assert(S::LOGSK == 8 && S::LUTK_OFF == 0 && S::KTAB == 65536, "byte-addressed key tables");
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int pos = (8 * j + 4 * u) * KB;
+            const uint32_t sel = (4u + ((pos >> 3) & 3)) << 8;
+            const uint32_t wv = bf.k[t][pos >> 5];
+            const uint2 eh = lds_at<uint2>(lds, __builtin_amdgcn_perm(wv, lutk_lane, 0x0c0c0000u | sel));
+            const uint2 el = lds_at<uint2>(lds, __builtin_amdgcn_perm(wv, lutk_lane | S::KTAB, 0x0c020000u | sel));
+            ah[2 * u] = eh.x, ah[2 * u + 1] = eh.y;
+            al[2 * u] = el.x, al[2 * u + 1] = el.y;
+          }
+        } else if constexpr (S::QUADK) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const uint32_t a = key_addr<4 * KB, S::LOGSK>(bf.k[t], (8 * j + 4 * u) * KB, lutk_lane, kmask);
