@@ -533,11 +533,19 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
 #pragma unroll
   for (int r = 0; r < NQ; ++r) qmax = fmaxf(qmax, s_qs[r]);
   const float sq = f16_split_scale(qmax);
-  u32x4_t qa[KPP], qb[KPP];
+  // With 4-row groups the hi and lo pieces share one operand: A rows 0..3
+  // hold the rows' hi parts, rows 4..7 their lo parts (rows 8..15 zero), so
+  // one MFMA per k step gives both products and a lane exchange adds them
+  // (PIECE_ROWS); 16-row groups keep a second operand for the lo parts.
+  constexpr bool PIECE_ROWS = 2 * NQ <= 16;
+  u32x4_t qa[KPP], qb[PIECE_ROWS ? 1 : KPP];
   {
-    // rows n >= NQ read row 0 and scale it by zero (no per-lane branches)
-    const float qsl = n < NQ ? sq : 0.f;
-    const float* y = s_q + (n < NQ ? n : 0) * S::QSTRIDE + g * S::KSPAN;
+    // rows past the group read row 0 and scale it by zero (no per-lane branches)
+    const int qrow = PIECE_ROWS ? (n < NQ ? n : n - NQ) : n;
+    const bool qok = PIECE_ROWS ? n < 2 * NQ : n < NQ;
+    const bool lo_row = PIECE_ROWS && n >= NQ;
+    const float qsl = qok ? sq : 0.f;
+    const float* y = s_q + (qok ? qrow : 0) * S::QSTRIDE + g * S::KSPAN;
 #pragma unroll
     for (int j = 0; j < KPP; ++j)
 #pragma unroll
@@ -545,8 +553,13 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
         uint32_t h0, l0, h1, l1;
         split_f16(y[4 * j + 2 * h] * qsl, h0, l0);
         split_f16(y[4 * j + 2 * h + 1] * qsl, h1, l1);
-        qa[j][2 * h] = qa[j][2 * h + 1] = h0 | (h1 << 16);
-        qb[j][2 * h] = qb[j][2 * h + 1] = l0 | (l1 << 16);
+        const uint32_t hp = h0 | (h1 << 16), lp = l0 | (l1 << 16);
+        if constexpr (PIECE_ROWS) {
+          qa[j][2 * h] = qa[j][2 * h + 1] = lo_row ? lp : hp;
+        } else {
+          qa[j][2 * h] = qa[j][2 * h + 1] = hp;
+          qb[j][2 * h] = qb[j][2 * h + 1] = lp;
+        }
       }
   }
   // scores in log2 units: S * ||k|| * log2(e) / (s_K s_Q); per register i
@@ -595,7 +608,7 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
 #pragma unroll
       for (int i = 0; i < KAL; ++i)
         al[tt][i] = S::KALIGNED ? bf.k[tt][i] : __builtin_amdgcn_alignbit(bf.k[tt][i + 1], bf.k[tt][i], ksh);
-    f32x4_t Sa[2], Sb[2];
+    f32x4_t Sa[2], Sb[2];  // (Sb: 16-row groups only)
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) Sa[tt] = Sb[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -612,11 +625,22 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         Sa[tt] = mfma_f16(qa[j], bk[tt], Sa[tt]);
-        Sb[tt] = mfma_f16(qb[j], bk[tt], Sb[tt]);
+        if constexpr (!PIECE_ROWS) Sb[tt] = mfma_f16(qb[j], bk[tt], Sb[tt]);
       }
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) Sc[tt] = Sa[tt] + Sb[tt];
+    for (int tt = 0; tt < 2; ++tt) {
+      if constexpr (PIECE_ROWS) {
+        // lane (g, token n) register i is A row 4 g + i: lanes of group 0
+        // hold the hi products of rows 0..3, group 1 the lo products; lanes
+        // n and n + 16 swap and add (groups 0 and 1 then both hold the rows'
+        // scores, groups 2 and 3 zeros, as the rows past the group did)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Sc[tt][i] = Sa[tt][i] + xor_lane<16>(Sa[tt][i]);
+      } else {
+        Sc[tt] = Sa[tt] + Sb[tt];
+      }
+    }
   };
   auto finish = [&](const Buf& bf, const f32x4_t (&Sc)[2], int s0) {
     float sv[2][4];  // scores in log2 units
