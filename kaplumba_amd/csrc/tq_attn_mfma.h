@@ -1,7 +1,7 @@
 // TurboQuant decode / verify attention straight from packed indices, with the
 // dot products on gfx950's matrix cores (v_mfma_f32_16x16x32_f16).
 //
-// Workgroup: 8 wave64s (two per SIMD; 4 for d = 256) own tokens [t_begin, t_end) of one kv
+// Workgroup: 8 wave64s (two per SIMD; 4 for d = 256 with 3- or 4-bit values) own tokens [t_begin, t_end) of one kv
 // head of one sequence and up to NQ (4 or 16) query rows of that head's GQA
 // group.  Tokens are cut into 32-token sub-chunks; sub-chunk i belongs to wave
 // i % 8 (i % 4).  Every wave keeps the global loads of its next P sub-chunks in flight
@@ -114,7 +114,9 @@ __device__ __forceinline__ float f16_split_scale(float maxabs) {
 template <int D, int KB, int VB, int NQ>
 struct MfmaShape {
   // d = 256 runs one wave per SIMD (512 registers each), smaller heads two
-  static constexpr int NW = D >= 256 ? 4 : 8;
+  // two waves per SIMD; d = 256 with 3- and 4-bit values one (their value
+  // words and tables do not fit 256 registers per wave)
+  static constexpr int NW = (D >= 256 && VB >= 3) ? 4 : 8;
   static constexpr int NT = NW * kWave;
   static constexpr int SUB = 32;  // tokens per sub-chunk
   static constexpr int P = 2;     // sub-chunks in flight per wave
@@ -155,7 +157,11 @@ struct MfmaShape {
   static constexpr int Q_OFF = BK + BV;   // [NQ][QSTRIDE] f32 rotated queries
   static constexpr int QS_OFF = Q_OFF + NQ * QSTRIDE * 4;  // [NQ] f32 max |q_rot| per row
   static constexpr int W_OFF = QS_OFF + 64;                // [NW][16][32] f16 weights
-  static constexpr int LOOP_BYTES = W_OFF + NW * 16 * SUB * 2;
+  // 4-row groups: the query A operands of every MFMA step, [KPP][64 lanes]
+  // x 16 B, shared by the waves (their rows are the same)
+  static constexpr bool QLDS = 2 * NQ <= 16;
+  static constexpr int QOP_OFF = W_OFF + NW * 16 * SUB * 2;
+  static constexpr int LOOP_BYTES = QOP_OFF + (QLDS ? KPP * kWave * 16 : 0);
   // after the token loop the buffers above are dead: the epilogue's buffers
   // start again at 0 (a barrier separates the two phases)
   static constexpr int CO_OFF = 0;                          // [NW][NQ][D] f32 wave outputs
@@ -249,9 +255,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 
 template <int D, int KB, int VB, int NQ>
 // block size: MfmaShape<D, KB, VB, NQ>::NT
-__global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__((MfmaShape<D, KB, VB, NQ>::NT), 1) void attn_mfma_kernel(AttnParams p) {
   using S = MfmaShape<D, KB, VB, NQ>;
-  static_assert(S::NT == (D >= 256 ? 256 : 512), "launch bounds");
   constexpr int NW = S::NW;
   constexpr int NT = S::NT;
   constexpr int SUB = S::SUB;
@@ -537,8 +542,8 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
   // hold the rows' hi parts, rows 4..7 their lo parts (rows 8..15 zero), so
   // one MFMA per k step gives both products and a lane exchange adds them
   // (PIECE_ROWS); 16-row groups keep a second operand for the lo parts.
-  constexpr bool PIECE_ROWS = 2 * NQ <= 16;
-  u32x4_t qa[KPP], qb[PIECE_ROWS ? 1 : KPP];
+  constexpr bool PIECE_ROWS = S::QLDS;
+  u32x4_t qa[PIECE_ROWS ? 1 : KPP], qb[PIECE_ROWS ? 1 : KPP];
   {
     // rows past the group read row 0 and scale it by zero (no per-lane branches)
     const int qrow = PIECE_ROWS ? (n < NQ ? n : n - NQ) : n;
@@ -555,7 +560,11 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
         split_f16(y[4 * j + 2 * h + 1] * qsl, h1, l1);
         const uint32_t hp = h0 | (h1 << 16), lp = l0 | (l1 << 16);
         if constexpr (PIECE_ROWS) {
-          qa[j][2 * h] = qa[j][2 * h + 1] = lo_row ? lp : hp;
+          // every wave forms the same operands: wave 0 stores them
+          if (wave == 0) {
+            uint32_t* qo = reinterpret_cast<uint32_t*>(lds + S::QOP_OFF + (j * kWave + lane) * 16);
+            qo[2 * h] = qo[2 * h + 1] = lo_row ? lp : hp;
+          }
         } else {
           qa[j][2 * h] = qa[j][2 * h + 1] = hp;
           qb[j][2 * h] = qb[j][2 * h + 1] = lp;
@@ -622,9 +631,14 @@ __global__ __launch_bounds__(D >= 256 ? 256 : 512, 1) void attn_mfma_kernel(Attn
           bk[tt][2 * h] = v.x;
           bk[tt][2 * h + 1] = v.y;
         }
+      u32x4_t aj;
+      if constexpr (PIECE_ROWS)
+        aj = lds_at<u32x4_t>(lds, S::QOP_OFF + (j * kWave + lane) * 16);
+      else
+        aj = qa[j];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        Sa[tt] = mfma_f16(qa[j], bk[tt], Sa[tt]);
+        Sa[tt] = mfma_f16(aj, bk[tt], Sa[tt]);
         if constexpr (!PIECE_ROWS) Sb[tt] = mfma_f16(qb[j], bk[tt], Sb[tt]);
       }
     }
