@@ -60,8 +60,56 @@ __device__ __forceinline__ void append_lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// v[I0 .. I0 + 7] += c * (the same register of lane ^ OFF): one v_fmac_f32 per
+// element, its first source read from the partner lane through DPP.  c is +-1,
+// so the product is exact and each result is one rounding of the sum.  A DPP
+// source needs two wait states after a VALU write of its register, and the
+// compiler does not look inside the block: hence the s_nop 1 on either side.
+#define TQ_FMAC_DPP8(CTRL)                                                                   \
+  asm("s_nop 1\n\t"                                                                          \
+      "v_fmac_f32_dpp %0, %0, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %1, %1, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %2, %2, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %3, %3, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %4, %4, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %5, %5, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %6, %6, %8 " CTRL "\n\t"                                               \
+      "v_fmac_f32_dpp %7, %7, %8 " CTRL "\n\t"                                               \
+      "s_nop 1"                                                                              \
+      : "+v"(v[I0]), "+v"(v[I0 + 1]), "+v"(v[I0 + 2]), "+v"(v[I0 + 3]), "+v"(v[I0 + 4]),   \
+        "+v"(v[I0 + 5]), "+v"(v[I0 + 6]), "+v"(v[I0 + 7])                                    \
+      : "v"(c))
+
+template <int OFF, int I0>
+__device__ __forceinline__ void fmac_xor8(float (&v)[32], float c) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 8, "one-instruction DPP lane xor");
+  if constexpr (OFF == 1) {
+    TQ_FMAC_DPP8("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf");
+  } else if constexpr (OFF == 2) {
+    TQ_FMAC_DPP8("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf");
+  } else {
+    TQ_FMAC_DPP8("row_ror:8 row_mask:0xf bank_mask:0xf");
+  }
+}
+#undef TQ_FMAC_DPP8
+
 // One block's share of a quantize launch: vectors [block * VPB, block * VPB + VPB)
 // of a (256 threads).  Shared by the one-tensor and the key + value kernels.
+//
+// Signs.  Multiplying by s_i = +-1 commutes exactly with the division by the
+// norm (IEEE division is sign-symmetric), so the signs are applied to the raw
+// input as sign-bit xors (two f16 / bf16 elements per instruction).  The same
+// xor also flips lane g's elements by (-1)^popcount(g): with that flip, every
+// cross-lane butterfly stage becomes v + c * partner with c = -1 on the lower
+// lane of a pair and +1 on the upper one (one DPP fma per element), and every
+// lane ends with the unflipped value.  Proof by induction over the stages: a
+// lane entering the stage of lane bit j holds its value times
+// (-1)^popcount(g >> j), and its partner the opposite sign, so the lower lane
+// forms a + b and the upper a - b times the lane's incoming sign, which is
+// (-1)^popcount(g >> (j + 1)) for both.  Results are bit-identical (rounding
+// to nearest is symmetric); at most the sign of a zero differs, which no
+// compare against a midpoint sees.  A sign vector with an entry other than
+// +-1 makes the block multiply by it after the division instead.
 template <int D, int BITS, int XDT>
 __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t block) {
   constexpr int NL = D / 32;          // lanes per vector
@@ -69,65 +117,115 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   constexpr int NMID = (1 << BITS) - 1;
   constexpr int PW = D * BITS / 32;
   constexpr bool LUT = NMID > 3;  // bucket table beyond three midpoints
-  constexpr int SPT = (D + 255) / 256;  // sign entries per thread
-  __shared__ float s_sign[D];
+  constexpr int EPW = XDT == TQ_DTYPE_F32 ? 1 : 2;  // elements per sign word
+  constexpr int SW = D / EPW;                        // sign words
+  constexpr int SPT = (SW + 255) / 256;              // sign words per thread
+  __shared__ __align__(16) uint32_t s_smask[SW];
   __shared__ float s_mid[NMID];
+  __shared__ uint32_t s_cell[LUT ? NMID : 1];
   __shared__ uint2 s_qb[LUT ? kQbN : 1];
-  __shared__ int s_qb_bad;
+  __shared__ int s_bad;  // bit 0: a sign is not +-1; bit 1: a table cell holds two midpoints
 
   // The block's small constants are requested first, then this lane's 32
   // input elements; the table set-up below runs while the rows are in flight.
-  float sgn[SPT];
+  float sgn[SPT][EPW];
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    sgn[k] = i < D ? a.rot[i] : 0.f;
+    const int w = threadIdx.x + 256 * k;
+#pragma unroll
+    for (int j = 0; j < EPW; ++j) sgn[k][j] = w < SW ? a.rot[w * EPW + j] : 1.f;
   }
   const float mid_t = threadIdx.x < NMID ? a.mid[threadIdx.x] : 0.f;
+  const QbGrid grid = qb_grid(a.mid[0], a.mid[NMID - 1]);
 
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
-  const int64_t vec = block * VPB + threadIdx.x / NL;
+  const int tv = threadIdx.x / NL;
+  const int64_t vec = block * VPB + tv;
   const int g = threadIdx.x % NL;
   const bool live = vec < n_vec;
-  // lanes past the last vector load vector 0 (launches have n_vec >= 1) and
-  // drop it: unconditional loads keep the wait counts exact
-  const int64_t vl = live ? vec : 0;
-  const int l = static_cast<int>(vl % a.L);
-  const int64_t bh = vl / a.L;
-  const int h = static_cast<int>(bh % a.H);
-  const int b = static_cast<int>(bh / a.H);
+  int l, h, b;
+  if (a.L % VPB == 0) {
+    // the block's vectors share one (b, h) row and are all live: the
+    // divisions are the block's, on uniform values
+    const int64_t bh = (block * VPB) / a.L;
+    l = static_cast<int>(block * VPB - bh * a.L) + tv;
+    h = static_cast<int>(bh % a.H);
+    b = static_cast<int>(bh / a.H);
+  } else {
+    // lanes past the last vector load vector 0 (launches have n_vec >= 1) and
+    // drop it: unconditional loads keep the wait counts exact
+    const int64_t vl = live ? vec : 0;
+    l = static_cast<int>(vl % a.L);
+    const int64_t bh = vl / a.L;
+    h = static_cast<int>(bh % a.H);
+    b = static_cast<int>(bh / a.H);
+  }
   constexpr int ES = XDT == TQ_DTYPE_F32 ? 4 : 2;
   Raw32<XDT> raw;
   load_raw32<XDT>(static_cast<const char*>(a.x) + (b * a.sb + h * a.sh + l * a.sl + g * 32) * ES, raw);
 
+  int bad = 0;
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    if (i < D) s_sign[i] = sgn[k];
+    const int w = threadIdx.x + 256 * k;
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < EPW; ++j) {
+      const int e = w * EPW + j;
+      bad |= fabsf(sgn[k][j]) != 1.f ? 1 : 0;
+      const bool flip = (sgn[k][j] < 0.f) != ((__popc(static_cast<uint32_t>(e) >> 5) & 1) != 0);
+      m |= flip ? (EPW == 1 ? 0x80000000u : (0x8000u << (16 * j))) : 0u;
+    }
+    if (w < SW) s_smask[w] = m;
+  }
+  if (threadIdx.x == 0) s_bad = 0;
+  if constexpr (LUT) {
+    if (threadIdx.x < NMID) s_cell[threadIdx.x] = qb_cell(mid_t, grid);
   }
   if (threadIdx.x < NMID) s_mid[threadIdx.x] = mid_t;
-  if (threadIdx.x == 0) s_qb_bad = 0;
   append_lds_barrier();
+  if (bad) atomicOr(&s_bad, 1);
   if constexpr (LUT) {
     for (int t = threadIdx.x; t < kQbN; t += blockDim.x) {
       uint2 ent;
-      if (!qb_entry(t, s_mid, NMID, ent)) s_qb_bad = 1;
+      if (!qb_entry(static_cast<uint32_t>(t), s_cell, s_mid, NMID, ent)) atomicOr(&s_bad, 2);
       s_qb[t] = ent;
     }
-    append_lds_barrier();
   }
-  const bool use_lut = LUT && s_qb_bad == 0;
+  append_lds_barrier();
+  const int bad_all = s_bad;
+  const bool sign_mul = (bad_all & 1) != 0;
+  const bool use_lut = LUT && (bad_all & 2) == 0 && grid.ok;
 
   // Every lane of a vector shares `vec`, so a vector's lanes leave together
   // and the xor-shuffles below stay inside live lane groups.
   if (!live) return;
+  {
+    const uint32_t flip0 = (__popc(static_cast<uint32_t>(g)) & 1) ? (EPW == 1 ? 0x80000000u : 0x80008000u) : 0u;
+    const uint4* mk = reinterpret_cast<const uint4*>(s_smask) + g * Raw32<XDT>::N;
+#pragma unroll
+    for (int i = 0; i < Raw32<XDT>::N; ++i) {
+      const uint4 m = sign_mul ? make_uint4(flip0, flip0, flip0, flip0) : mk[i];
+      raw.w[i].x ^= m.x;
+      raw.w[i].y ^= m.y;
+      raw.w[i].z ^= m.z;
+      raw.w[i].w ^= m.w;
+    }
+  }
   float v[32];
   widen32<XDT>(raw, v);
 
-  // ---- norm: in-lane fold 16, 8, 4, 2, 1 then cross-lane xor butterfly
+  // ---- norm: in-lane fold 16, 8, 4, 2, 1 then cross-lane xor butterfly.  The
+  // square of an f16 value is exact in f32 (22 significand bits, exponent in
+  // range), so the first fold's RN(a^2 + RN(b^2)) equals RN(RN(a^2) + RN(b^2)).
   float s[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = __fadd_rn(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 16], v[i + 16]));
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (XDT == TQ_DTYPE_F16)
+      s[i] = __builtin_fmaf(v[i], v[i], __fmul_rn(v[i + 16], v[i + 16]));
+    else
+      s[i] = __fadd_rn(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 16], v[i + 16]));
+  }
 #pragma unroll
   for (int w = 8; w >= 1; w >>= 1) {
 #pragma unroll
@@ -141,11 +239,12 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   const float n = sqrt_rn(ss);
   const float den = fmaxf(n, kNormEps);
 
-  // ---- normalise (IEEE x / den, div_by_norm) and apply signs (multiplying
-  // by +-1 is exact)
+  // ---- normalise (IEEE x / den, div_by_norm); the signs are already in
   div_by_norm<XDT>(v, den, v);
+  if (sign_mul) {
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = __fmul_rn(v[i], s_sign[g * 32 + i]);
+    for (int i = 0; i < 32; ++i) v[i] = __fmul_rn(v[i], a.rot[g * 32 + i]);
+  }
 
   // ---- Walsh-Hadamard: in-lane stages (distance 1..16)
 #pragma unroll
@@ -160,14 +259,20 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
       }
     }
   }
-  // ---- cross-lane stages (distance 32, 64, ...): lane bit j <-> element bit 5+j;
-  // the upper lane of a pair forms p - v, the lower v + p, both as one
-  // rounding of v * (+-1) + p (the product is exact)
+  // ---- cross-lane stages (distance 32, 64, ...): lane bit j <-> element bit
+  // 5 + j; v + c * partner with c = -1 on the lower lane, +1 on the upper
   auto cross = [&](auto off_tag) {
     constexpr int OFF = decltype(off_tag)::value;
-    const float sg = (g & OFF) != 0 ? -1.f : 1.f;
+    const float c = (g & OFF) != 0 ? 1.f : -1.f;
+    if constexpr (OFF == 1 || OFF == 2 || OFF == 8) {
+      fmac_xor8<OFF, 0>(v, c);
+      fmac_xor8<OFF, 8>(v, c);
+      fmac_xor8<OFF, 16>(v, c);
+      fmac_xor8<OFF, 24>(v, c);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = __builtin_fmaf(v[i], sg, xor_lane<OFF>(v[i]));
+      for (int i = 0; i < 32; ++i) v[i] = __builtin_fmaf(xor_lane<OFF>(v[i]), c, v[i]);
+    }
   };
   if constexpr (NL >= 2) cross(std::integral_constant<int, 1>{});
   if constexpr (NL >= 4) cross(std::integral_constant<int, 2>{});
@@ -192,7 +297,7 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   // a NaN / infinite norm makes every y NaN, and NaN compares below every midpoint
   if (use_lut && n < INFINITY) {
     pack_all([&](float y) -> uint32_t {
-      const uint2 ent = s_qb[qb_index(y)];
+      const uint2 ent = s_qb[qb_cell(y, grid)];
       return ent.x + ((y > __uint_as_float(ent.y)) ? 1u : 0u);
     });
   } else {

@@ -120,46 +120,46 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 
 // ------------------------------------------------- quantization buckets ----
 // idx(y) = #{m : y > mid_m} for sorted midpoints through one table lookup.
-// y is bucketed by bits 30..20 of its magnitude (the 8 exponent bits and the
-// top 3 mantissa bits: a monotone image of |y|), clamped so that bucket 0
-// holds |y| < 2^-24 and the last bucket |y| >= 2 (and inf / NaN); negative y
-// use a mirrored copy, so the table index is monotone in y.  Entry t holds
-// (number of midpoints below the bucket, the midpoint inside it or +inf);
-// the lookup is exact whenever no bucket holds two midpoints (the buckets are
-// 1/8 of a binade wide, Lloyd-Max midpoints are much farther apart), which
+// y goes to cell(y) = trunc(clamp(fma(y, k, c), 0, kQbN - 1)), a monotone
+// function of y; k and c spread the midpoints over cells 1 .. kQbN - 1.
+// Entry j holds (the number of midpoints in cells below j, the midpoint in
+// cell j or +inf).  For every y with cell(y) = j, a midpoint in a lower cell
+// is below y and one in a higher cell above it (monotonicity), so the lookup
+// plus one compare is exact whenever no cell holds two midpoints, which
 // qb_entry reports so that a kernel can fall back to plain comparisons.
-constexpr uint32_t kQbLo = 823;                 // (bits >> 20) of 2^-24 is 824
-constexpr uint32_t kQbHi = 1024;                // (bits >> 20) of 2.0
-constexpr int kQbHalf = kQbHi - kQbLo + 1;      // 202 buckets per sign
-constexpr int kQbN = 2 * kQbHalf;               // 404 table entries
+constexpr int kQbN = 256;
 
-__device__ __forceinline__ uint32_t qb_index(float y) {
-  const uint32_t u = __float_as_uint(y);
-  const uint32_t e = min(max((u >> 20) & 0x7ffu, kQbLo), kQbHi) - kQbLo;  // 0 .. 201
-  const uint32_t sm = static_cast<uint32_t>(static_cast<int32_t>(u) >> 31);
-  return kQbHalf + (e ^ sm);  // y >= +0: 202 + e; y <= -0: 202 + ~e = 201 - e
+struct QbGrid {
+  float k, c;
+  bool ok;  // finite, increasing
+};
+
+__device__ __forceinline__ QbGrid qb_grid(float lo, float hi) {
+  QbGrid g;
+  g.k = static_cast<float>(kQbN - 2) / (hi - lo);
+  g.c = 1.f - lo * g.k;
+  g.ok = g.k > 0.f && g.k < INFINITY && fabsf(g.c) < INFINITY;
+  return g;
 }
 
-// Table entry t for the nmid sorted midpoints; returns false when two
-// midpoints share the bucket.
-__device__ __forceinline__ bool qb_entry(int t, const float* mid, int nmid, uint2& ent) {
-  const bool neg = t < kQbHalf;
-  const int e = neg ? (kQbHalf - 1 - t) : (t - kQbHalf);
-  const float alo = e == 0 ? 0.f : __uint_as_float((static_cast<uint32_t>(e) + kQbLo) << 20);
-  const float ahi = e == static_cast<int>(kQbHi - kQbLo)
-                        ? INFINITY
-                        : __uint_as_float((static_cast<uint32_t>(e) + kQbLo + 1) << 20);
+__device__ __forceinline__ uint32_t qb_cell(float y, const QbGrid& g) {
+  const float t = fminf(fmaxf(__builtin_fmaf(y, g.k, g.c), 0.f), static_cast<float>(kQbN - 1));
+  return static_cast<uint32_t>(t);
+}
+
+// Table entry t from the midpoints' cells; returns false when two midpoints
+// share cell t.
+__device__ __forceinline__ bool qb_entry(uint32_t t, const uint32_t* cell, const float* mid, int nmid,
+                                         uint2& ent) {
   uint32_t base = 0;
   int inside = 0;
   float thr = INFINITY;
   for (int m = 0; m < nmid; ++m) {
-    const float md = mid[m];
-    if (!neg) {  // y in [alo, ahi)
-      if (md < alo) ++base;
-      else if (md < ahi) { ++inside; thr = md; }
-    } else {     // y in (-ahi, -alo]
-      if (md <= -ahi) ++base;
-      else if (md <= -alo) { ++inside; thr = md; }
+    const uint32_t cm = cell[m];
+    base += cm < t ? 1u : 0u;
+    if (cm == t) {
+      ++inside;
+      thr = mid[m];
     }
   }
   ent = make_uint2(base, __float_as_uint(thr));

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import tq_oracle as O
-from kaplumba_amd import ops
+from kaplumba_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -155,6 +155,82 @@ def test_config0_full_layer_bit_exact(device):
         xf = x.astype(np.float64)
         cos = (deq * xf).sum(-1) / (np.linalg.norm(deq, axis=-1) * np.linalg.norm(xf, axis=-1))
         assert cos.mean() > 0.97
+
+
+def _append_raw(x, bits, rot, mids, packed, norms, offset=0):
+    """tq_append_quantize with caller-chosen sign vector and midpoints."""
+    B, H, L, D = x.shape
+    rc = _lib.load().tq_append_quantize(
+        x.data_ptr(), _lib.torch_dtype_code(x.dtype), B, H, L, D,
+        x.stride(0), x.stride(1), x.stride(2), bits, _lib.TQ_ROT_HADAMARD,
+        rot.data_ptr(), mids.data_ptr(), packed.data_ptr(), norms.data_ptr(),
+        _lib.torch_dtype_code(norms.dtype), packed.shape[2], offset, ops._stream(x))
+    _lib.check(rc, "tq_append_quantize")
+
+
+def _quantize_mids(x, bits, signs, mids):
+    """The oracle's quantize with explicit midpoints."""
+    xf = np.asarray(x, np.float32)
+    n = O.norm_f32(xf)
+    u = xf / np.maximum(n, O.EPS)[..., None]
+    return O.pack_lowbit(O.quantize_indices(O.rht_forward_f32(u, signs), mids), bits), n
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128, 256, 512])
+def test_sign_vector_with_non_unit_entries(device, dtype, d):
+    """Signs other than +-1 are multiplied after the division, as the oracle does."""
+    rng = np.random.default_rng(d + 7)
+    signs = O.rht_signs(d, 3).astype(np.float32)
+    signs[rng.choice(d, 5, replace=False)] = np.array([0.5, -2.0, 0.0, -0.25, 3.0], np.float32)
+    x = rng.standard_normal((1, 4, 70, d)).astype(np.float32)
+    xt = torch.from_numpy(x).to(dtype)
+    xin = xt.float().numpy()
+    for bits in (2, 3, 4):
+        mids = O.midpoints(O.beta_codebook(d, bits))
+        codec = ops.Codec(d, bits, 3)
+        packed, norms = _buffers(1, 4, 70, codec, torch.float32, device)
+        _append_raw(xt.to(device), bits, torch.from_numpy(signs).to(device),
+                    torch.from_numpy(mids).to(device), packed, norms)
+        wp, wn = _quantize_mids(xin, bits, signs, mids)
+        assert np.array_equal(_np_u32(packed), wp), bits
+        assert np.array_equal(norms.cpu().numpy(), wn), bits
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_midpoints_sharing_a_table_cell(device, bits):
+    """Two midpoints closer than a table cell: the kernel compares against every midpoint.
+
+    Also midpoints at 0 and at +-tiny values, and inputs whose coordinates land on
+    midpoints exactly (one-hot vectors put +-1/sqrt(D) on every coordinate)."""
+    d = 128
+    rng = np.random.default_rng(bits)
+    nm = (1 << bits) - 1
+    base = np.sort(rng.uniform(-0.25, 0.25, nm)).astype(np.float32)
+    close = base.copy()
+    close[nm // 2] = np.float32(1e-7)
+    close[nm // 2 + 1] = np.float32(3e-7)
+    exact = base.copy()
+    exact[nm // 2] = np.float32(0.0)
+    exact[nm // 2 - 1] = -O.rht_scale(d)
+    exact[nm // 2 + 1] = O.rht_scale(d)
+    exact = np.sort(exact).astype(np.float32)
+    x = rng.standard_normal((1, 2, 64, d)).astype(np.float32)
+    x[0, 0, :8] = 0.0
+    for j in range(8):
+        x[0, 0, j, 3 * j] = 1.0 + j
+    x[0, 1, 0] = 0.0
+    signs = O.rht_signs(d, 1)
+    for mids in (np.sort(close), exact):
+        mids = mids.astype(np.float32)
+        codec = ops.Codec(d, bits, 1)
+        packed, norms = _buffers(1, 2, 64, codec, torch.float32, device)
+        xt = torch.from_numpy(x).to(torch.float16)
+        _append_raw(xt.to(device), bits, torch.from_numpy(signs).to(device),
+                    torch.from_numpy(mids).to(device), packed, norms)
+        wp, wn = _quantize_mids(xt.float().numpy(), bits, signs, mids)
+        assert np.array_equal(_np_u32(packed), wp)
+        assert np.array_equal(norms.cpu().numpy(), wn)
 
 
 @pytest.mark.parametrize("d,bits", [(64, 2), (128, 3), (256, 4)])
