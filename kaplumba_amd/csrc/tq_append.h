@@ -18,6 +18,12 @@ struct AppendArgs {
   float scale;         // f32(1/sqrt(D)), Hadamard only
 };
 
+// Workgroup barrier over LDS only: outstanding global loads stay in flight
+// across it (__syncthreads would wait for them too).
+__device__ __forceinline__ void append_lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // u[i] = x[i] / den with IEEE (correctly rounded) division, den = max(n, 1e-6)
 // the vector's norm.  The quotient comes from the correctly rounded
 // reciprocal r = RN(1 / den), one division per vector: q = RN(x r) is within

@@ -54,12 +54,6 @@ __device__ __forceinline__ void widen32(const Raw32<DT>& r, float (&v)[32]) {
   }
 }
 
-// Workgroup barrier over LDS only: outstanding global loads stay in flight
-// across it (__syncthreads would wait for them too).
-__device__ __forceinline__ void append_lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // v[I0 .. I0 + 7] += c * (the same register of lane ^ OFF): one v_fmac_f32 per
 // element, its first source read from the partner lane through DPP.  c is +-1,
 // so the product is exact and each result is one rounding of the sum.  A DPP

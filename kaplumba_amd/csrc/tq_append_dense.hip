@@ -10,9 +10,13 @@
 // once per workgroup into three bf16 pieces R = R0 + R1 + R2 (each the
 // round-to-nearest-even bf16 of what the previous pieces leave; together they
 // carry R's full 24-bit significand), x enters as bf16 (exact for bf16 input;
-// f16 input is the exact sum of two bf16 pieces and f32 input the sum of three),
-// every piece product is exact and the sum runs in f32.  Products whose piece
-// orders add up to more than 2 are below f32 resolution and skipped.  Instead
+// f32 input is the exact sum of three bf16 pieces), every piece product is
+// exact and the sum runs in f32.  Products whose piece orders add up to more
+// than 2 are below f32 resolution and skipped.  f16 input feeds
+// v_mfma_f32_32x32x16_f16 exactly as loaded, against three f16 pieces of
+// 2^rs R, where 2^rs brings the workgroup's largest |R| entry into
+// [2^14, 2^15): three products per tile and k-step instead of five, and no
+// split of x.  The scale is exact and is applied to the thresholds too.  Instead
 // of dividing, each coordinate is compared with mid_m * max(n, eps), computed
 // once per vector.  The result therefore differs from an f32 `u @ R^T` only in
 // the last bits of the sum, so an index can differ only where y lies within a
@@ -70,7 +74,29 @@ __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x16_t mfma32h(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Split a and b into NP f16 pieces each (round to nearest even, exact f32
+// remainders), packed per piece as (a_i, b_i).
+template <int NP>
+__device__ __forceinline__ void split_f16x2(float a, float b, uint32_t (&w)[NP]) {
+  float ra = a, rb = b;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const f16x2_t v = {static_cast<_Float16>(ra), static_cast<_Float16>(rb)};
+    w[i] = __builtin_bit_cast(uint32_t, v);
+    ra = __fsub_rn(ra, static_cast<float>(v[0]));
+    rb = __fsub_rn(rb, static_cast<float>(v[1]));
+  }
+}
 
 // Split a and b into NP bf16 pieces each (round-to-nearest-even, exact
 // remainders), packed per piece as (a_i, b_i): one v_cvt_pk_bf16_f32 per piece
@@ -111,6 +137,12 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
   constexpr int PW = D * BITS / 32;
   constexpr int NX = S::LE * XP::ES / 16;  // 16-byte loads per lane
 
+  // f16 input feeds f16 MFMAs as loaded (one x piece); R then goes into f16
+  // pieces, scaled by 2^rs so that the largest entry sits just below 2^15.
+  constexpr bool HX = XDT == TQ_DTYPE_F16;
+  constexpr int NXP = HX ? 1 : XP::N;
+  __shared__ uint32_t s_rmax;
+
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
@@ -127,11 +159,21 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
   // keep the compiler's wait counts exact.
   auto load_x = [&](int64_t tile, u32x4_t (&xr)[NX], int64_t& row) {
     const int64_t vec = tile * S::VPT + wave * 32 + vl;
-    const int64_t vc = vec < n_vec ? vec : 0;
-    const int l = static_cast<int>(vc % a.L);
-    const int64_t bh = vc / a.L;
-    const int h = static_cast<int>(bh % a.H);
-    const int b = static_cast<int>(bh / a.H);
+    int l, h, b;
+    if (a.L % S::VPT == 0) {
+      // the tile's vectors share one (b, h) row and are all live: the
+      // divisions are the tile's, on uniform values
+      const int64_t bh = (tile * S::VPT) / a.L;
+      l = static_cast<int>(tile * S::VPT - bh * a.L) + wave * 32 + vl;
+      h = static_cast<int>(bh % a.H);
+      b = static_cast<int>(bh / a.H);
+    } else {
+      const int64_t vc = vec < n_vec ? vec : 0;
+      l = static_cast<int>(vc % a.L);
+      const int64_t bh = vc / a.L;
+      h = static_cast<int>(bh % a.H);
+      b = static_cast<int>(bh / a.H);
+    }
     const int64_t xoff = b * a.sb + h * a.sh + l * a.sl + g * S::LE;
     const u32x4_t* src =
         reinterpret_cast<const u32x4_t*>(static_cast<const char*>(a.x) + xoff * XP::ES);
@@ -139,6 +181,11 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
     for (int i = 0; i < NX; ++i) xr[i] = src[i];
     row = vec < n_vec ? (static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l : -1;
   };
+
+  if constexpr (HX) {
+    if (tid == 0) s_rmax = 0u;
+    append_lds_barrier();
+  }
 
   // ---- R pieces -> LDS in A-fragment order.  This thread's fragments are
   // requested first, then its first input tile, so the tile's loads are in
@@ -163,6 +210,21 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
   u32x4_t xr[NX];
   int64_t row;
   load_x(tile, xr, row);
+  // 2^rs: the power of two that brings the workgroup's largest |R| entry into
+  // [2^14, 2^15) (2^15 for an all-zero R); exact, and undone on the thresholds
+  float r_scale = 1.f;
+  if constexpr (HX) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < FPT; ++i)
+      m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(rv[i][0].x), fabsf(rv[i][0].y)), fmaxf(fabsf(rv[i][0].z), fabsf(rv[i][0].w))),
+                         fmaxf(fmaxf(fabsf(rv[i][1].x), fabsf(rv[i][1].y)), fmaxf(fabsf(rv[i][1].z), fabsf(rv[i][1].w)))));
+    atomicMax(&s_rmax, __float_as_uint(m));  // non-negative floats order as their bits
+    append_lds_barrier();
+    int e = 0;
+    frexpf(__uint_as_float(s_rmax), &e);  // max < 2^e
+    r_scale = ldexpf(1.f, min(max(15 - e, -100), 100));
+  }
 #pragma unroll
   for (int i = 0; i < FPT; ++i) {
     const int f = tid + i * kDenseThreads;
@@ -172,7 +234,10 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t pr[S::NRP];
-      split_bf16x2<S::NRP>(e[2 * j], e[2 * j + 1], pr);
+      if constexpr (HX)
+        split_f16x2<S::NRP>(__fmul_rn(e[2 * j], r_scale), __fmul_rn(e[2 * j + 1], r_scale), pr);
+      else
+        split_bf16x2<S::NRP>(e[2 * j], e[2 * j + 1], pr);
 #pragma unroll
       for (int p = 0; p < S::NRP; ++p) w[p][j] = pr[p];
     }
@@ -183,6 +248,7 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
   float mid[NMID];
 #pragma unroll
   for (int m = 0; m < NMID; ++m) mid[m] = GE ? 0.f : a.mid[m];
+
   __syncthreads();
 
   for (; tile * S::VPT < n_vec; tile += tile_stride) {
@@ -196,7 +262,8 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
       for (int i = 0; i < 16; ++i) {
         const float u0 = x_elem<XDT, NX>(xr, 32 * q + i);
         const float u1 = x_elem<XDT, NX>(xr, 32 * q + i + 16);
-        s[i] = __fadd_rn(__fmul_rn(u0, u0), __fmul_rn(u1, u1));
+        // f16 squares are exact in f32: RN(a^2 + RN(b^2)) = RN(RN(a^2) + RN(b^2))
+        s[i] = HX ? __builtin_fmaf(u0, u0, __fmul_rn(u1, u1)) : __fadd_rn(__fmul_rn(u0, u0), __fmul_rn(u1, u1));
       }
 #pragma unroll
       for (int w = 8; w >= 1; w >>= 1) {
@@ -215,7 +282,7 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
     const float den = fmaxf(n, kNormEps);
     float thr[NMID];
 #pragma unroll
-    for (int m = 0; m < NMID; ++m) thr[m] = __fmul_rn(mid[m], den);
+    for (int m = 0; m < NMID; ++m) thr[m] = __fmul_rn(__fmul_rn(mid[m], den), r_scale);
 
     // ---- x @ R^T for this slice's coordinates
     f32x16_t acc[S::NT];
@@ -223,8 +290,8 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
     for (int t = 0; t < S::NT; ++t) acc[t] = f32x16_t{};
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
-      u32x4_t xb[XP::N];
-      if constexpr (XDT == TQ_DTYPE_BF16) {
+      u32x4_t xb[NXP];
+      if constexpr (XDT == TQ_DTYPE_BF16 || HX) {
         xb[0] = xr[ks];
       } else {
 #pragma unroll
@@ -239,11 +306,13 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
 #pragma unroll
       for (int rp = S::NRP - 1; rp >= 0; --rp) {
 #pragma unroll
-        for (int xp = XP::N - 1; xp >= 0; --xp) {
+        for (int xp = NXP - 1; xp >= 0; --xp) {
           if (rp + xp > 2) continue;
 #pragma unroll
-          for (int t = 0; t < S::NT; ++t)
-            acc[t] = mfma32(s_r[((rp * S::NT + t) * S::KS + ks) * kWave + lane], xb[xp], acc[t]);
+          for (int t = 0; t < S::NT; ++t) {
+            const u32x4_t ra = s_r[((rp * S::NT + t) * S::KS + ks) * kWave + lane];
+            acc[t] = HX ? mfma32h(ra, xb[xp], acc[t]) : mfma32(ra, xb[xp], acc[t]);
+          }
         }
       }
       // keep each k-step's fragment reads next to its products (hoisting all
@@ -251,53 +320,62 @@ __device__ __forceinline__ void dense_body(const AppendArgs& a, u32x4_t* s_r, in
       __builtin_amdgcn_sched_barrier(0);
     }
 
+    // ---- the next tile's input is requested now (x is dead after the
+    // products), so its loads are in flight during the quantize and stores
+    const int64_t row_cur = row;
+    if ((tile + tile_stride) * S::VPT < n_vec) load_x(tile + tile_stride, xr, row);
+
     // ---- quantize against mid * max(n, eps), pack 32 coordinates per lane and pair
-    if (row >= 0) {
-      uint32_t* dst_row = a.packed + row * PW;
+    if (row_cur >= 0) {
+      uint32_t* dst_row = a.packed + row_cur * PW;
+      auto pack_pairs = [&](auto idx_of) {
 #pragma unroll
-      for (int p = 0; p < S::NT / 2; ++p) {
-        uint32_t words[BITS];
+        for (int p = 0; p < S::NT / 2; ++p) {
+          uint32_t words[BITS];
 #pragma unroll
-        for (int w = 0; w < BITS; ++w) words[w] = 0u;
+          for (int w = 0; w < BITS; ++w) words[w] = 0u;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-          const float y = acc[2 * p + e / 16][e % 16];
-          uint32_t idx = 0;
-          if constexpr (NMID >= 7) {
-            // thr is sorted, so the middle threshold decides which half
-            // can still hold y: count that half (H compares, its thresholds
-            // chosen by H selects) on top of the H + 1 below it or none.
-            // The same count as NMID compares, in 2H + 2 fewer operations.
-            constexpr int H = NMID / 2;
-            const bool up = GE ? (y >= thr[H]) : (y > thr[H]);
-            idx = up ? static_cast<uint32_t>(H + 1) : 0u;
-#pragma unroll
-            for (int m = 0; m < H; ++m) {
-              const float t = up ? thr[H + 1 + m] : thr[m];
-              idx += (GE ? (y >= t) : (y > t)) ? 1u : 0u;
-            }
-          } else {
-#pragma unroll
-            for (int m = 0; m < NMID; ++m) idx += (GE ? (y >= thr[m]) : (y > thr[m])) ? 1u : 0u;
+          for (int e = 0; e < 32; ++e) {
+            const uint32_t idx = idx_of(acc[2 * p + e / 16][e % 16]);
+            const int pos = e * BITS;
+            const int wi = pos >> 5;
+            const int sh = pos & 31;
+            words[wi] |= idx << sh;
+            if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
           }
-          const int pos = e * BITS;
-          const int wi = pos >> 5;
-          const int sh = pos & 31;
-          words[wi] |= idx << sh;
-          if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
-        }
-        uint32_t* dst = dst_row + ((c0 + 64 * p + 32 * g) / 32) * BITS;
+          uint32_t* dst = dst_row + ((c0 + 64 * p + 32 * g) / 32) * BITS;
 #pragma unroll
-        for (int w = 0; w < BITS; ++w) dst[w] = words[w];
-      }
+          for (int w = 0; w < BITS; ++w) dst[w] = words[w];
+        }
+      };
+      pack_pairs([&](float y) -> uint32_t {
+        uint32_t idx = 0;
+        if constexpr (NMID >= 7) {
+          // thr is sorted, so the middle threshold decides which half
+          // can still hold y: count that half (H compares, its thresholds
+          // chosen by H selects) on top of the H + 1 below it or none.
+          // The same count as NMID compares, in 2H + 2 fewer operations.
+          constexpr int H = NMID / 2;
+          const bool up = GE ? (y >= thr[H]) : (y > thr[H]);
+          idx = up ? static_cast<uint32_t>(H + 1) : 0u;
+#pragma unroll
+          for (int m = 0; m < H; ++m) {
+            const float t = up ? thr[H + 1 + m] : thr[m];
+            idx += (GE ? (y >= t) : (y > t)) ? 1u : 0u;
+          }
+        } else {
+#pragma unroll
+          for (int m = 0; m < NMID; ++m) idx += (GE ? (y >= thr[m]) : (y > thr[m])) ? 1u : 0u;
+        }
+        return idx;
+      });
       if (slice == 0 && g == 0) {
         if (a.norm_dtype == TQ_DTYPE_F16)
-          static_cast<uint16_t*>(a.norms)[row] = f32_to_f16_bits(n);
+          static_cast<uint16_t*>(a.norms)[row_cur] = f32_to_f16_bits(n);
         else
-          static_cast<float*>(a.norms)[row] = n;
+          static_cast<float*>(a.norms)[row_cur] = n;
       }
     }
-    if ((tile + tile_stride) * S::VPT < n_vec) load_x(tile + tile_stride, xr, row);
   }
 }
 

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import tq_oracle as O
-from kaplumba_amd import ops
+from kaplumba_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -138,3 +138,38 @@ def test_dense_config3_layer(device):
     xf = xin.astype(np.float64)
     cos = (deq * xf).sum(-1) / (np.linalg.norm(deq, axis=-1) * np.linalg.norm(xf, axis=-1))
     assert cos.mean() > 0.97
+
+
+@pytest.mark.parametrize("scale", [1.0, 300.0, 2.0 ** -13, 3e4])
+def test_dense_f16_rotation_of_any_scale(device, scale):
+    """f16 input runs f16 products against a power-of-two-scaled split of R: any
+    magnitude of R gives the oracle's indices (band scaled with R)."""
+    d, bits = 128, 3
+    rng = np.random.default_rng(int(scale * 7) % 1000)
+    R = (O.rotation_matrix(d, 2) * np.float32(scale)).astype(np.float32)
+    R[3, 5] = np.float32(scale * 0.9)   # one large entry next to small ones
+    x = _synth(rng, (1, 4, 96, d)).astype(np.float16)
+    cb = O.beta_codebook(d, bits)
+    mids = O.midpoints(cb)
+    codec = ops.Codec(d, bits, 0, rotation="dense")
+    packed, norms = _buffers(1, 4, 96, codec, torch.float32, device)
+    xt = torch.from_numpy(x).to(device)
+    rt = torch.from_numpy(R).to(device)
+    mt = torch.from_numpy(mids).to(device)
+    rc = _lib.load().tq_append_quantize(
+        xt.data_ptr(), _lib.torch_dtype_code(xt.dtype), 1, 4, 96, d,
+        xt.stride(0), xt.stride(1), xt.stride(2), bits, _lib.TQ_ROT_DENSE,
+        rt.data_ptr(), mt.data_ptr(),
+        packed.data_ptr(), norms.data_ptr(), _lib.torch_dtype_code(norms.dtype), 96, 0, ops._stream(xt))
+    _lib.check(rc, "tq_append_quantize")
+    torch.cuda.synchronize()
+    wp, wn, y = O.quantize_dense(x.astype(np.float32), bits, R, cb)
+    assert np.array_equal(norms.cpu().numpy(), wn)
+    gi = O.unpack_lowbit(packed.cpu().numpy().astype(np.uint32), bits, d).astype(np.int64)
+    wi = O.unpack_lowbit(wp, bits, d).astype(np.int64)
+    bad = gi != wi
+    if bad.any():
+        dist = np.abs(y[bad].astype(np.float64)[:, None] - mids.astype(np.float64)[None, :]).min(axis=1)
+        assert dist.max() <= BAND * max(1.0, scale)
+        assert np.abs(gi[bad] - wi[bad]).max() == 1
+    assert int(bad.sum()) <= 2
