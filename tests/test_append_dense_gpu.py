@@ -173,3 +173,20 @@ def test_dense_f16_rotation_of_any_scale(device, scale):
         assert dist.max() <= BAND * max(1.0, scale)
         assert np.abs(gi[bad] - wi[bad]).max() == 1
     assert int(bad.sum()) <= 2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dense_whole_tiles_batched(device, dtype):
+    """L a multiple of the 256-vector tile (the row indices are then the tile's):
+    several (b, h) rows, model-layout strides, an offset inside the capacity."""
+    rng = np.random.default_rng(17)
+    B, H, L, d, bits = 2, 3, 512, 128, 3
+    x = _synth(rng, (B, H, L, d))
+    xt = torch.from_numpy(x).to(dtype).transpose(1, 2).contiguous().transpose(1, 2).to(device)
+    codec = ops.Codec(d, bits, 0, rotation="dense")
+    packed, norms = _buffers(B, H, L + 5, codec, torch.float32, device)
+    ops.append_quantize(xt, codec, packed, norms, 3)
+    gp = packed.cpu().numpy().astype(np.uint32)
+    flips = _check(xt.float().cpu().numpy(), bits, d, 0, gp[:, :, 3:3 + L], norms.cpu().numpy()[:, :, 3:3 + L])
+    assert flips <= 2
+    assert not gp[:, :, :3].any() and not gp[:, :, 3 + L:].any()

@@ -233,6 +233,24 @@ def test_midpoints_sharing_a_table_cell(device, bits):
         assert np.array_equal(norms.cpu().numpy(), wn)
 
 
+@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
+def test_whole_row_blocks_batched(device, d):
+    """L a multiple of every block size (the row indices are then the block's):
+    several (b, h) rows, model-layout strides, an offset inside the capacity."""
+    rng = np.random.default_rng(d + 3)
+    B, H, L, bits = 2, 3, 256, 3
+    x32, _ = _synth(rng, (B, H, L, d), torch.float16)
+    xt = torch.from_numpy(x32).to(torch.float16).transpose(1, 2).contiguous().transpose(1, 2).to(device)
+    codec = ops.Codec(d, bits, 4)
+    packed, norms = _buffers(B, H, L + 9, codec, torch.float32, device)
+    ops.append_quantize(xt, codec, packed, norms, offset=7)
+    wp, wn = O.quantize_rht(xt.float().cpu().numpy(), bits, O.rht_signs(d, 4), O.beta_codebook(d, bits))
+    gp = _np_u32(packed)
+    assert np.array_equal(gp[:, :, 7:7 + L], wp)
+    assert np.array_equal(norms.cpu().numpy()[:, :, 7:7 + L], wn)
+    assert not gp[:, :, :7].any() and not gp[:, :, 7 + L:].any()
+
+
 @pytest.mark.parametrize("d,bits", [(64, 2), (128, 3), (256, 4)])
 def test_dequantize_matches_oracle(device, d, bits):
     rng = np.random.default_rng(d)
