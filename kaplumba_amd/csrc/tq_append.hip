@@ -28,6 +28,10 @@ struct Raw32 {
   uint4 w[N];
 };
 
+__device__ __forceinline__ uint32_t u4_word(const uint4& u, int k) {
+  return k == 0 ? u.x : (k == 1 ? u.y : (k == 2 ? u.z : u.w));
+}
+
 template <int DT>
 __device__ __forceinline__ void load_raw32(const void* p, Raw32<DT>& r) {
   const uint4* q = static_cast<const uint4*>(p);
@@ -116,9 +120,9 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   constexpr int SPT = (SW + 255) / 256;              // sign words per thread
   __shared__ __align__(16) uint32_t s_smask[SW];
   __shared__ float s_mid[NMID];
-  __shared__ uint32_t s_cell[LUT ? NMID : 1];
+  __shared__ float s_thr[LUT ? NMID : 1];  // the midpoints moved before the scale (unscaled_threshold)
   __shared__ uint2 s_qb[LUT ? kQbN : 1];
-  __shared__ int s_bad;  // bit 0: a sign is not +-1; bit 1: a table cell holds two midpoints
+  __shared__ int s_bad;  // bit 0: a sign is not +-1; bit 1: no exact table
 
   // The block's small constants are requested first, then this lane's 32
   // input elements; the table set-up below runs while the rows are in flight.
@@ -130,7 +134,6 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
     for (int j = 0; j < EPW; ++j) sgn[k][j] = w < SW ? a.rot[w * EPW + j] : 1.f;
   }
   const float mid_t = threadIdx.x < NMID ? a.mid[threadIdx.x] : 0.f;
-  const QbGrid grid = qb_grid(a.mid[0], a.mid[NMID - 1]);
 
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
   const int tv = threadIdx.x / NL;
@@ -174,15 +177,23 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   }
   if (threadIdx.x == 0) s_bad = 0;
   if constexpr (LUT) {
-    if (threadIdx.x < NMID) s_cell[threadIdx.x] = qb_cell(mid_t, grid);
+    // the table indexes the Hadamard output v before the scale: v > T_m
+    // exactly when RN(v * scale) > mid_m
+    if (threadIdx.x < NMID) {
+      float T = 0.f;
+      if (!unscaled_threshold(mid_t, a.scale, T)) bad |= 2;
+      s_thr[threadIdx.x] = T;
+    }
   }
   if (threadIdx.x < NMID) s_mid[threadIdx.x] = mid_t;
   append_lds_barrier();
-  if (bad) atomicOr(&s_bad, 1);
+  if (bad) atomicOr(&s_bad, bad);
+  QbGrid grid{};
   if constexpr (LUT) {
+    grid = qb_grid(s_thr[0], s_thr[NMID - 1]);
     for (int t = threadIdx.x; t < kQbN; t += blockDim.x) {
       uint2 ent;
-      if (!qb_entry(static_cast<uint32_t>(t), s_cell, s_mid, NMID, ent)) atomicOr(&s_bad, 2);
+      if (!qb_entry_grid(static_cast<uint32_t>(t), s_thr, NMID, grid, ent)) atomicOr(&s_bad, 2);
       s_qb[t] = ent;
     }
   }
@@ -207,7 +218,7 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
     }
   }
   float v[32];
-  widen32<XDT>(raw, v);
+  if constexpr (XDT != TQ_DTYPE_F16) widen32<XDT>(raw, v);
 
   // ---- norm: in-lane fold 16, 8, 4, 2, 1 then cross-lane xor butterfly.  The
   // square of an f16 value is exact in f32 (22 significand bits, exponent in
@@ -215,10 +226,15 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   float s[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    if constexpr (XDT == TQ_DTYPE_F16)
-      s[i] = __builtin_fmaf(v[i], v[i], __fmul_rn(v[i + 16], v[i + 16]));
-    else
+    if constexpr (XDT == TQ_DTYPE_F16) {
+      // element i is half (i & 1) of word i / 2 of the lane's 16 (raw.w[i / 8])
+      const uint32_t wa = u4_word(raw.w[i / 8], (i / 2) % 4), wb = u4_word(raw.w[(i + 16) / 8], ((i + 16) / 2) % 4);
+      const float a0 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((i & 1) ? (wa >> 16) : wa)));
+      const float b0 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((i & 1) ? (wb >> 16) : wb)));
+      s[i] = __builtin_fmaf(a0, a0, __builtin_fmaf(b0, b0, 0.f));  // b^2 >= 0: adding +0 keeps it
+    } else {
       s[i] = __fadd_rn(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 16], v[i + 16]));
+    }
   }
 #pragma unroll
   for (int w = 8; w >= 1; w >>= 1) {
@@ -233,8 +249,30 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   const float n = sqrt_rn(ss);
   const float den = fmaxf(n, kNormEps);
 
-  // ---- normalise (IEEE x / den, div_by_norm); the signs are already in
-  div_by_norm<XDT>(v, den, v);
+  // ---- normalise (IEEE x / den, div_by_norm); the signs are already in.
+  // f16 input: the two fmas that read x take it as an f16 source straight
+  // from the packed words (v_fma_mix_f32, either half), so no element is
+  // converted on its own; q = fma(x, r, +0) is RN(x r) for every x != 0 (x r
+  // is a normal number), and for x = +-0 both forms end in u = +0.
+  if constexpr (XDT == TQ_DTYPE_F16) {
+    const float r = __fdiv_rn(1.f, den);
+#pragma unroll
+    for (int i = 0; i < Raw32<XDT>::N; ++i) {
+      const uint32_t w[4] = {raw.w[i].x, raw.w[i].y, raw.w[i].z, raw.w[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float q0, q1, e0, e1;
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(q0) : "v"(w[j]), "v"(r));
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(q1) : "v"(w[j]), "v"(r));
+        asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(e0) : "v"(q0), "v"(den), "v"(w[j]));
+        asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(e1) : "v"(q1), "v"(den), "v"(w[j]));
+        v[8 * i + 2 * j] = __builtin_fmaf(e0, r, q0);
+        v[8 * i + 2 * j + 1] = __builtin_fmaf(e1, r, q1);
+      }
+    }
+  } else {
+    div_by_norm<XDT>(v, den, v);
+  }
   if (sign_mul) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) v[i] = __fmul_rn(v[i], a.rot[g * 32 + i]);
@@ -273,29 +311,35 @@ __device__ __forceinline__ void rht_quantize_block(const AppendArgs& a, int64_t 
   if constexpr (NL >= 8) cross(std::integral_constant<int, 4>{});
   if constexpr (NL >= 16) cross(std::integral_constant<int, 8>{});
 
-  // ---- scale, quantize against midpoints, pack thread-locally
+  // ---- quantize against midpoints, pack thread-locally (one shift-or per
+  // index: v_lshl_or_b32)
   uint32_t words[BITS];
   auto pack_all = [&](auto idx_of) {
+    // all indices first (the table reads batch), then the shift-ors
+    uint32_t ix[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ix[i] = idx_of(v[i]);
 #pragma unroll
     for (int w = 0; w < BITS; ++w) words[w] = 0u;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      const uint32_t idx = idx_of(__fmul_rn(v[i], a.scale));
+      const uint32_t idx = ix[i];
       const int pos = i * BITS;
       const int wi = pos >> 5;
       const int sh = pos & 31;
-      words[wi] |= idx << sh;
+      asm("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(words[wi]) : "v"(idx), "i"(sh), "v"(words[wi]));
       if (sh + BITS > 32) words[wi + 1] |= idx >> (32 - sh);
     }
   };
   // a NaN / infinite norm makes every y NaN, and NaN compares below every midpoint
   if (use_lut && n < INFINITY) {
-    pack_all([&](float y) -> uint32_t {
-      const uint2 ent = s_qb[qb_cell(y, grid)];
-      return ent.x + ((y > __uint_as_float(ent.y)) ? 1u : 0u);
+    pack_all([&](float x) -> uint32_t {
+      const uint2 ent = s_qb[qb_cell(x, grid)];
+      return ent.x + ((x > __uint_as_float(ent.y)) ? 1u : 0u);
     });
   } else {
-    pack_all([&](float y) -> uint32_t {
+    pack_all([&](float x) -> uint32_t {
+      const float y = __fmul_rn(x, a.scale);
       uint32_t idx = 0;
 #pragma unroll
       for (int m = 0; m < NMID; ++m) idx += (y > s_mid[m]) ? 1u : 0u;

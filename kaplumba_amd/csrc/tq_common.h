@@ -166,6 +166,50 @@ __device__ __forceinline__ bool qb_entry(uint32_t t, const uint32_t* cell, const
   return inside <= 1;
 }
 
+// Neighbouring floats of a finite t (+-0 count as one value).
+__device__ __forceinline__ float next_up(float t) {
+  if (t == 0.f) return __uint_as_float(1u);
+  const uint32_t u = __float_as_uint(t);
+  return __uint_as_float(t > 0.f ? u + 1u : u - 1u);
+}
+__device__ __forceinline__ float next_down(float t) { return -next_up(-t); }
+
+// The largest float T with RN(T * s) <= mid, for s > 0: then RN(v * s) > mid
+// exactly when v > T (RN(v * s) is monotone in v), so a compare against T
+// replaces the product.  A walk of a few ulps from RN(mid / s); midpoints at
+// or near zero walk up through the subnormals (about 2^-150 / s / 2^-149
+// steps, under 32 for s >= 2^-6).  Returns false when the walk does not
+// settle (the caller then compares RN(v * s) itself).
+__device__ __forceinline__ bool unscaled_threshold(float mid, float s, float& T) {
+  if (!(fabsf(mid) < INFINITY) || !(s > 0.f) || !(s < INFINITY)) return false;
+  float t = __fdiv_rn(mid, s);
+  if (!(fabsf(t) < INFINITY)) return false;
+  for (int k = 0; k < 4 && __fmul_rn(t, s) > mid; ++k) t = next_down(t);
+  for (int k = 0; k < 32 && __fmul_rn(next_up(t), s) <= mid; ++k) t = next_up(t);
+  T = t;
+  return __fmul_rn(t, s) <= mid && __fmul_rn(next_up(t), s) > mid;
+}
+
+// Table entry t from thresholds thr[0 .. n) (cells taken with grid g);
+// returns false when two of them share cell t.
+__device__ __forceinline__ bool qb_entry_grid(uint32_t t, const float* thr, int n, const QbGrid& g,
+                                              uint2& ent) {
+  uint32_t base = 0;
+  int inside = 0;
+  float tm = INFINITY;
+  for (int m = 0; m < n; ++m) {
+    const float th = thr[m];
+    const uint32_t cm = qb_cell(th, g);
+    base += cm < t ? 1u : 0u;
+    if (cm == t) {
+      ++inside;
+      tm = th;
+    }
+  }
+  ent = make_uint2(base, __float_as_uint(tm));
+  return inside <= 1;
+}
+
 // Lane value of the partner lane ^ OFF (OFF < 32), all in the vector ALU
 // (no LDS round trip): DPP inside a row of 16 lanes, the gfx950 row swap
 // across rows.
