@@ -126,7 +126,7 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 // cell j or +inf).  For every y with cell(y) = j, a midpoint in a lower cell
 // is below y and one in a higher cell above it (monotonicity), so the lookup
 // plus one compare is exact whenever no cell holds two midpoints, which
-// qb_entry reports so that a kernel can fall back to plain comparisons.
+// qb_entry_grid reports so that a kernel can fall back to plain comparisons.
 constexpr int kQbN = 256;
 
 struct QbGrid {
@@ -145,25 +145,6 @@ __device__ __forceinline__ QbGrid qb_grid(float lo, float hi) {
 __device__ __forceinline__ uint32_t qb_cell(float y, const QbGrid& g) {
   const float t = fminf(fmaxf(__builtin_fmaf(y, g.k, g.c), 0.f), static_cast<float>(kQbN - 1));
   return static_cast<uint32_t>(t);
-}
-
-// Table entry t from the midpoints' cells; returns false when two midpoints
-// share cell t.
-__device__ __forceinline__ bool qb_entry(uint32_t t, const uint32_t* cell, const float* mid, int nmid,
-                                         uint2& ent) {
-  uint32_t base = 0;
-  int inside = 0;
-  float thr = INFINITY;
-  for (int m = 0; m < nmid; ++m) {
-    const uint32_t cm = cell[m];
-    base += cm < t ? 1u : 0u;
-    if (cm == t) {
-      ++inside;
-      thr = mid[m];
-    }
-  }
-  ent = make_uint2(base, __float_as_uint(thr));
-  return inside <= 1;
 }
 
 // Neighbouring floats of a finite t (+-0 count as one value).
