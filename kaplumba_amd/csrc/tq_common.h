@@ -120,8 +120,13 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 
 // ------------------------------------------------- quantization buckets ----
 // idx(y) = #{m : y > mid_m} for sorted midpoints through one table lookup.
-// y goes to cell(y) = trunc(clamp(fma(y, k, c), 0, kQbN - 1)), a monotone
-// function of y; k and c spread the midpoints over cells 1 .. kQbN - 1.
+// y goes to cell(y) = clamp(round(y k + c), 0, kQbN - 1), a monotone function
+// of y; k and c spread the midpoints over cells 1 .. kQbN - 1.  The rounding
+// is the float's own: t = RN(y k + c + 1.5 * 2^23) is an integer-valued float
+// in [2^23, 2^24) while |y k + c| < 2^22, whose bits are those of
+// 1.5 * 2^23 plus the integer; outside that range the bits (as int32) lie
+// below or above the clamp bounds, so one integer clamp of the bits finishes
+// the cell (fma, med3, and the table address).
 // Entry j holds (the number of midpoints in cells below j, the midpoint in
 // cell j or +inf).  For every y with cell(y) = j, a midpoint in a lower cell
 // is below y and one in a higher cell above it (monotonicity), so the lookup
@@ -129,22 +134,25 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 // qb_entry_grid reports so that a kernel can fall back to plain comparisons.
 constexpr int kQbN = 256;
 
+constexpr int kQbMagic = 0x4B400000;  // bits of 1.5 * 2^23
+
 struct QbGrid {
-  float k, c;
-  bool ok;  // finite, increasing
+  float k, c;  // c includes 1.5 * 2^23
+  bool ok;     // finite, increasing
 };
 
 __device__ __forceinline__ QbGrid qb_grid(float lo, float hi) {
   QbGrid g;
   g.k = static_cast<float>(kQbN - 2) / (hi - lo);
-  g.c = 1.f - lo * g.k;
-  g.ok = g.k > 0.f && g.k < INFINITY && fabsf(g.c) < INFINITY;
+  const float c0 = 1.f - lo * g.k;
+  g.c = c0 + 0x1.8p23f;
+  g.ok = g.k > 0.f && g.k < INFINITY && fabsf(c0) < 0x1p20f;
   return g;
 }
 
 __device__ __forceinline__ uint32_t qb_cell(float y, const QbGrid& g) {
-  const float t = fminf(fmaxf(__builtin_fmaf(y, g.k, g.c), 0.f), static_cast<float>(kQbN - 1));
-  return static_cast<uint32_t>(t);
+  const int t = __float_as_int(__builtin_fmaf(y, g.k, g.c));
+  return static_cast<uint32_t>(min(max(t, kQbMagic), kQbMagic + kQbN - 1) - kQbMagic);
 }
 
 // Neighbouring floats of a finite t (+-0 count as one value).
