@@ -370,10 +370,17 @@ __global__ __launch_bounds__(256) void append_rht_kernel(AppendArgs a) {
 // (launch, first-load latency, tail) of a decode or prefill append.
 template <int D, int KBITS, int VBITS, int XDT>
 __global__ __launch_bounds__(256) void append_rht_kv_kernel(AppendArgs k, AppendArgs v, int64_t k_blocks) {
-  if (static_cast<int64_t>(blockIdx.x) < k_blocks)
-    rht_quantize_block<D, KBITS, XDT>(k, blockIdx.x);
-  else
-    rht_quantize_block<D, VBITS, XDT>(v, blockIdx.x - k_blocks);
+  const bool key = static_cast<int64_t>(blockIdx.x) < k_blocks;
+  if constexpr (KBITS == VBITS) {
+    // one copy of the body for both sides (the side's arguments picked
+    // first): half the code for the instruction cache
+    rht_quantize_block<D, KBITS, XDT>(key ? k : v, key ? blockIdx.x : blockIdx.x - k_blocks);
+  } else {
+    if (key)
+      rht_quantize_block<D, KBITS, XDT>(k, blockIdx.x);
+    else
+      rht_quantize_block<D, VBITS, XDT>(v, blockIdx.x - k_blocks);
+  }
 }
 
 // ------------------------------------------------------------------ plain ---
