@@ -18,6 +18,29 @@ struct AppendArgs {
   float scale;         // f32(1/sqrt(D)), Hadamard only
 };
 
+// a or b, field by field (each field a uniform select: the result stays in
+// scalar registers, where picking a whole kernel argument makes a copy in
+// scratch memory)
+__device__ __forceinline__ AppendArgs select_args(bool pick_a, const AppendArgs& a, const AppendArgs& b) {
+  AppendArgs r;
+  r.x = pick_a ? a.x : b.x;
+  r.sb = pick_a ? a.sb : b.sb;
+  r.sh = pick_a ? a.sh : b.sh;
+  r.sl = pick_a ? a.sl : b.sl;
+  r.B = pick_a ? a.B : b.B;
+  r.H = pick_a ? a.H : b.H;
+  r.L = pick_a ? a.L : b.L;
+  r.rot = pick_a ? a.rot : b.rot;
+  r.mid = pick_a ? a.mid : b.mid;
+  r.packed = pick_a ? a.packed : b.packed;
+  r.norms = pick_a ? a.norms : b.norms;
+  r.norm_dtype = pick_a ? a.norm_dtype : b.norm_dtype;
+  r.cap = pick_a ? a.cap : b.cap;
+  r.offset = pick_a ? a.offset : b.offset;
+  r.scale = pick_a ? a.scale : b.scale;
+  return r;
+}
+
 // Workgroup barrier over LDS only: outstanding global loads stay in flight
 // across it (__syncthreads would wait for them too).
 __device__ __forceinline__ void append_lds_barrier() {

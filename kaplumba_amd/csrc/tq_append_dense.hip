@@ -391,10 +391,18 @@ __global__ __launch_bounds__(kDenseThreads) void append_dense_kernel(AppendArgs 
 template <int D, int KBITS, int VBITS, int XDT>
 __global__ __launch_bounds__(kDenseThreads) void append_dense_kv_kernel(AppendArgs k, AppendArgs v, int nk) {
   __shared__ u32x4_t s_r[DenseShape<D>::SLOTS];
-  if (static_cast<int>(blockIdx.x) < nk)
-    dense_body<D, KBITS, XDT, false>(k, s_r, blockIdx.x, nk);
-  else
-    dense_body<D, VBITS, XDT, false>(v, s_r, blockIdx.x - nk, gridDim.x - nk);
+  const bool key = static_cast<int>(blockIdx.x) < nk;
+  if constexpr (KBITS == VBITS) {
+    // one copy of the body for both sides (the side's arguments picked
+    // first): half the code for the instruction cache
+    const AppendArgs side = select_args(key, k, v);
+    dense_body<D, KBITS, XDT, false>(side, s_r, key ? blockIdx.x : blockIdx.x - nk, key ? nk : gridDim.x - nk);
+  } else {
+    if (key)
+      dense_body<D, KBITS, XDT, false>(k, s_r, blockIdx.x, nk);
+    else
+      dense_body<D, VBITS, XDT, false>(v, s_r, blockIdx.x - nk, gridDim.x - nk);
+  }
 }
 
 template <int D, int BITS>
