@@ -173,7 +173,9 @@ __device__ __forceinline__ bool unscaled_threshold(float mid, float s, float& T)
   if (!(fabsf(mid) < INFINITY) || !(s > 0.f) || !(s < INFINITY)) return false;
   float t = __fdiv_rn(mid, s);
   if (!(fabsf(t) < INFINITY)) return false;
+#pragma unroll 1
   for (int k = 0; k < 4 && __fmul_rn(t, s) > mid; ++k) t = next_down(t);
+#pragma unroll 1
   for (int k = 0; k < 32 && __fmul_rn(next_up(t), s) <= mid; ++k) t = next_up(t);
   T = t;
   return __fmul_rn(t, s) <= mid && __fmul_rn(next_up(t), s) > mid;
