@@ -71,8 +71,9 @@ int tq_packed_width(int dim, int bits);
  *   idx_i = #{ m : y_i > midpoints[m] }   (2^bits - 1 ascending midpoints)
  * and writes the packed row and the norm at token position offset + l of the
  * (b, h) row of the destination buffers (capacity tokens per (b, h)).
- * Hadamard: dim a power of two in [32, 512].  Dense: dim a multiple of 8 in
- * [8, 512] (64 / 128 / 256 on the matrix cores, other dims on the vector ALUs).
+ * Hadamard: dim a power of two in [32, 512].  Dense: any dim in [8, 512]
+ * (64 / 128 / 256 on the matrix cores, other dims on the vector ALUs).  x and
+ * its strides must be 16-byte aligned when dim is a multiple of 8.
  * bits in 1..4.  x_dtype: F32/F16/BF16.  norm_dtype: F32 or F16.
  */
 int tq_append_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
@@ -105,7 +106,8 @@ int tq_append_quantize_kv(const void* k_x, const void* v_x, int x_dtype, int B, 
  * Append L tokens unquantized into an fp16/bf16 layer buffer (the
  * mixed-precision layers).  Replaces the slice assignment of
  * KVCache.update_and_fetch (cache.py:415-441).  dtype: F16 or BF16; x and dst
- * share it.  dst is [B, H, capacity, dim].
+ * share it.  dst is [B, H, capacity, dim].  Any dim >= 1 (16-byte copies when
+ * dim is a multiple of 8 and the rows are 16-byte aligned, else per element).
  */
 int tq_append_plain(const void* x, int dtype, int B, int H, int L, int dim,
                     int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_l,
@@ -192,7 +194,7 @@ int64_t tq_attention_prod_workspace_size(int B, int Hq, int Hkv, int L, int dim,
  * seq_lens: NULL (every sequence holds max_tokens tokens) or a device int32
  *   array of B lengths, each <= max_tokens (ragged batches).
  * q: [B, Hq, L, dim] with element strides; out: contiguous [B, Hq, L, dim].
- * dim: multiples of 8 in 8..512 (powers of two for the Hadamard rotation);
+ * dim: 8..512 (powers of two for the Hadamard rotation);
  * 64 / 128 / 256 run the tuned kernels, other dims the kernels of
  * tq_attention_general.  L >= 1; Hq % Hkv == 0.
  * workspace: >= tq_attention_workspace_size() bytes, 256-byte aligned, no

@@ -392,7 +392,8 @@ struct PlainArgs {
   int64_t cap, offset;
 };
 
-// One thread copies 8 elements (16 bytes); D is a multiple of 8.
+// One thread copies 8 elements (16 bytes); D is a multiple of 8 and the rows
+// are 16-byte aligned.
 __global__ __launch_bounds__(256) void append_plain_kernel(PlainArgs a) {
   const int per_row = a.D / 8;
   const int64_t total = static_cast<int64_t>(a.B) * a.H * a.L * per_row;
@@ -409,6 +410,21 @@ __global__ __launch_bounds__(256) void append_plain_kernel(PlainArgs a) {
                    a.dst + ((static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l) * a.D) +
                c;
   *dst = *src;
+}
+
+// Any other dim or alignment: one thread per element.
+__global__ __launch_bounds__(256) void append_plain_elem_kernel(PlainArgs a) {
+  const int64_t total = static_cast<int64_t>(a.B) * a.H * a.L * a.D;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int d = static_cast<int>(i % a.D);
+  const int64_t vec = i / a.D;
+  const int l = static_cast<int>(vec % a.L);
+  const int64_t bh = vec / a.L;
+  const int h = static_cast<int>(bh % a.H);
+  const int b = static_cast<int>(bh / a.H);
+  a.dst[((static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l) * a.D + d] =
+      a.x[b * a.sb + h * a.sh + l * a.sl + d];
 }
 
 // ------------------------------------------------------------- dequantize ---
@@ -565,8 +581,10 @@ int check_append(const void* x, int x_dtype, int B, int H, int L, int dim, int64
   }
   if (!x || !rot || !midpoints || !packed || !norms)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append: null pointer");
+  // the vector-load kernels (every dim that is a multiple of 8) need 16-byte
+  // rows; other dims run the general kernel, which loads single elements
   const int es = x_dtype == TQ_DTYPE_F32 ? 4 : 2;
-  if (!aligned16(x) || (sb * es) % 16 || (sh * es) % 16 || (sl * es) % 16)
+  if (dim % 8 == 0 && (!aligned16(x) || (sb * es) % 16 || (sh * es) % 16 || (sl * es) % 16))
     return fail(TQ_ERR_INVALID_ARGUMENT, "append: x and its strides must be 16-byte aligned");
   a = AppendArgs{x, sb, sh, sl, B, H, L, rot, midpoints, packed, norms, norm_dtype, capacity, offset,
                  static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim)))};
@@ -645,21 +663,25 @@ extern "C" int tq_append_plain(const void* x, int dtype, int B, int H, int L, in
                                void* dst, int64_t capacity, int64_t offset, void* stream) {
   if (dtype != TQ_DTYPE_F16 && dtype != TQ_DTYPE_BF16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: dtype %d (F16/BF16 only)", dtype);
-  if (B < 0 || H < 0 || L < 0 || dim <= 0 || dim % 8)
-    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: bad shape (dim %% 8 == 0 required)");
+  if (B < 0 || H < 0 || L < 0 || dim <= 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: bad shape");
   if (offset < 0 || offset + L > capacity)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: tokens exceed capacity");
   if (static_cast<int64_t>(B) * H * L == 0) return TQ_OK;
   if (!x || !dst) return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: null pointer");
-  if (!aligned16(x) || !aligned16(dst) || (x_stride_b * 2) % 16 || (x_stride_h * 2) % 16 ||
-      (x_stride_l * 2) % 16)
-    return fail(TQ_ERR_INVALID_ARGUMENT, "append_plain: 16-byte alignment required");
   PlainArgs a{static_cast<const uint16_t*>(x), x_stride_b, x_stride_h, x_stride_l, B, H, L, dim,
               static_cast<uint16_t*>(dst), capacity, offset};
-  const int64_t total = static_cast<int64_t>(B) * H * L * (dim / 8);
-  hipLaunchKernelGGL(append_plain_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
+  if (dim % 8 == 0 && aligned16(x) && aligned16(dst) && (x_stride_b * 2) % 16 == 0 &&
+      (x_stride_h * 2) % 16 == 0 && (x_stride_l * 2) % 16 == 0) {
+    const int64_t total = static_cast<int64_t>(B) * H * L * (dim / 8);
+    hipLaunchKernelGGL(append_plain_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    return check_launch("append_plain_kernel");
+  }
+  const int64_t total = static_cast<int64_t>(B) * H * L * dim;
+  hipLaunchKernelGGL(append_plain_elem_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
                      dim3(256), 0, static_cast<hipStream_t>(stream), a);
-  return check_launch("append_plain_kernel");
+  return check_launch("append_plain_elem_kernel");
 }
 
 extern "C" int tq_dequantize(const uint32_t* packed, const void* norms, int norm_dtype, int B,
@@ -667,8 +689,8 @@ extern "C" int tq_dequantize(const uint32_t* packed, const void* norms, int norm
                              const float* codebook, int rot_kind, const float* rot, float* out,
                              void* stream) {
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: bits %d", bits);
-  if (dim < 8 || dim > 512 || dim % 8)
-    return fail(TQ_ERR_UNSUPPORTED, "dequantize: dim %d (multiples of 8 up to 512)", dim);
+  if (dim < 8 || dim > 512)
+    return fail(TQ_ERR_UNSUPPORTED, "dequantize: dim %d (8..512)", dim);
   if (rot_kind == TQ_ROT_HADAMARD && (dim & (dim - 1)))
     return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: Hadamard rotation needs a power-of-two dim, got %d", dim);
   if (T < 0 || T > capacity) return fail(TQ_ERR_INVALID_ARGUMENT, "dequantize: T > capacity");

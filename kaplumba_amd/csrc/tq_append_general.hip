@@ -1,6 +1,6 @@
 // Append-time quantize with the dense rotation, and dequantize, at any head
-// dim the fixed-size kernels do not cover (multiples of 8 up to 512: the
-// dims that are not powers of two take the dense rotation in the reference,
+// dim the fixed-size kernels do not cover (8..512: the dims that are not
+// powers of two take the dense rotation in the reference,
 // _TurboQuantMSECodec.__init__, turboquant_cache.py:4122-4139).
 //
 // Quantize (turboquant_cache.py:4186-4254, array path :4248-4254) per vector:
@@ -11,7 +11,7 @@
 //     the xor-butterfly order;
 //   * n = sqrt (IEEE), u = x / max(n, 1e-6) (IEEE division);
 //   * y = u @ R^T with f32 fused multiply-adds in four interleaved partial
-//     sums (coordinates d mod 4) added pairwise at the end;
+//     sums (coordinates d mod 4, in order of d) added pairwise at the end;
 //   * idx = #{m : y > mid[m]}; LSB-first packing into ceil(D*bits/32) words.
 // One workgroup of 256 threads owns 16 vectors: x and u stay in LDS, thread j
 // forms output coordinate j of all 16 vectors from row j of R (R crosses L2
@@ -105,13 +105,16 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
   }
   __syncthreads();
   // y = u @ R^T, indices
+  // a row of R is 16-byte aligned when D % 4 == 0 (R itself is); other
+  // dims read it one element at a time and finish with the D % 4 last
+  // coordinates (partial sums 0, 1, 2: u is zero past D in LDS)
+  const bool r_vec4 = (D & 3) == 0;
   for (int j = tid; j < D; j += 256) {
     float4 acc[kGaVec];
 #pragma unroll
     for (int v = 0; v < kGaVec; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4* r4 = reinterpret_cast<const float4*>(a.rot + static_cast<int64_t>(j) * D);
-    for (int m = 0; m < D / 4; ++m) {
-      const float4 r = r4[m];
+    const float* rrow = a.rot + static_cast<int64_t>(j) * D;
+    auto fma4 = [&](int m, float4 r) {
 #pragma unroll
       for (int v = 0; v < kGaVec; ++v) {
         const float4 u = reinterpret_cast<const float4*>(s_u[v])[m];
@@ -119,6 +122,23 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
         acc[v].y = __builtin_fmaf(u.y, r.y, acc[v].y);
         acc[v].z = __builtin_fmaf(u.z, r.z, acc[v].z);
         acc[v].w = __builtin_fmaf(u.w, r.w, acc[v].w);
+      }
+    };
+    if (r_vec4) {
+      const float4* r4 = reinterpret_cast<const float4*>(rrow);
+      for (int m = 0; m < D / 4; ++m) fma4(m, r4[m]);
+    } else {
+      for (int m = 0; m < D / 4; ++m)
+        fma4(m, make_float4(rrow[4 * m], rrow[4 * m + 1], rrow[4 * m + 2], rrow[4 * m + 3]));
+      const int d0 = D & ~3;
+      const float r0 = rrow[d0];  // D % 4 >= 1 here
+      const float r1 = (D & 3) > 1 ? rrow[d0 + 1] : 0.f;
+      const float r2 = (D & 3) > 2 ? rrow[d0 + 2] : 0.f;
+#pragma unroll
+      for (int v = 0; v < kGaVec; ++v) {
+        acc[v].x = __builtin_fmaf(s_u[v][d0], r0, acc[v].x);
+        if ((D & 3) > 1) acc[v].y = __builtin_fmaf(s_u[v][d0 + 1], r1, acc[v].y);
+        if ((D & 3) > 2) acc[v].z = __builtin_fmaf(s_u[v][d0 + 2], r2, acc[v].z);
       }
     }
 #pragma unroll
@@ -221,8 +241,8 @@ __global__ __launch_bounds__(256) void dequant_general_kernel(DequantGeneralArgs
 }  // namespace
 
 int launch_append_dense_general(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st) {
-  if (dim < 8 || dim > kGaMaxDim || dim % 8)
-    return fail(TQ_ERR_UNSUPPORTED, "append: dense rotation at dim %d (multiples of 8 up to 512)", dim);
+  if (dim < 8 || dim > kGaMaxDim)
+    return fail(TQ_ERR_UNSUPPORTED, "append: dense rotation at dim %d (8..512)", dim);
   if ((reinterpret_cast<uintptr_t>(a.rot) & 15u) != 0)
     return fail(TQ_ERR_INVALID_ARGUMENT, "append: dense rotation matrix must be 16-byte aligned");
   switch (bits) {

@@ -84,6 +84,9 @@ __global__ __launch_bounds__(kGenThreads) void gen_qprep_kernel(GenParams p, int
     const int c = tid % 64;
     const int jq = tid / 64;
     const int col = blockIdx.y * 64 + c;
+    // quarter jq of the 4-coordinate groups; the last quarter also takes the
+    // Dk % 4 coordinates past them (rows of mat are 16-byte aligned only when
+    // Dk % 4 == 0: other dims read them one element at a time)
     const int n4 = Dk / 4;
     const int a4 = jq * n4 / 4;
     const int b4 = (jq + 1) * n4 / 4;
@@ -91,9 +94,11 @@ __global__ __launch_bounds__(kGenThreads) void gen_qprep_kernel(GenParams p, int
 #pragma unroll
     for (int r = 0; r < kQpRows; ++r) acc[r] = 0.f;
     if (col < Dk) {
-      const float4* mrow = reinterpret_cast<const float4*>(mat + static_cast<int64_t>(col) * Dk);
+      const float* mr = mat + static_cast<int64_t>(col) * Dk;
+      const bool vec4 = (Dk & 3) == 0;
       for (int m = a4; m < b4; ++m) {
-        const float4 rv = mrow[m];
+        const float4 rv = vec4 ? reinterpret_cast<const float4*>(mr)[m]
+                               : make_float4(mr[4 * m], mr[4 * m + 1], mr[4 * m + 2], mr[4 * m + 3]);
 #pragma unroll
         for (int r = 0; r < kQpRows; ++r) {
           const float4 qv = s_q4[r * (DkP / 4) + m];
@@ -103,6 +108,12 @@ __global__ __launch_bounds__(kGenThreads) void gen_qprep_kernel(GenParams p, int
           acc[r] = fmaf(qv.w, rv.w, acc[r]);
         }
       }
+      if (jq == 3)
+        for (int d = 4 * n4; d < Dk; ++d) {
+          const float rv = mr[d];
+#pragma unroll
+          for (int r = 0; r < kQpRows; ++r) acc[r] = fmaf(s_q[r * DkP + d], rv, acc[r]);
+        }
     }
 #pragma unroll
     for (int r = 0; r < kQpRows; ++r) s_part[jq][r][c] = acc[r];
@@ -268,6 +279,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_partial_kernel(GenParams p) {
   const int vsh = vbit & 31;
   const bool vtwo = VB == 3 && vw0 + 1 < p.vpw;
   const int G = DkP / 32;
+  const bool k_vec8 = (Dk & 7) == 0;  // plain key rows 16-byte aligned
 
   for (int64_t t0 = t_begin; t0 < t_end; t0 += TT) {
     const int n = static_cast<int>(min<int64_t>(TT, t_end - t0));
@@ -282,8 +294,21 @@ __global__ __launch_bounds__(kGenThreads) void gen_partial_kernel(GenParams p) {
         const uint16_t* kr = static_cast<const uint16_t*>(p.k) + (rowbase + tr) * Dk + 32 * g;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
+          // 8 keys in one 16-byte load when Dk % 8 == 0 (rows 16-byte
+          // aligned); else one element at a time, zeros past Dk
           uint4 h = make_uint4(0, 0, 0, 0);
-          if (tv && 32 * g + 8 * u < Dk) h = reinterpret_cast<const uint4*>(kr)[u];
+          const int c0 = 32 * g + 8 * u;
+          if (tv && c0 < Dk) {
+            if (k_vec8) {
+              h = reinterpret_cast<const uint4*>(kr)[u];
+            } else {
+              uint32_t e16[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) e16[e] = c0 + e < Dk ? kr[8 * u + e] : 0u;
+              h = make_uint4(e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16),
+                             e16[6] | (e16[7] << 16));
+            }
+          }
           const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -407,7 +432,15 @@ __global__ __launch_bounds__(kGenThreads) void gen_partial_kernel(GenParams p) {
           const int64_t trow = rowbase + t0 + tt;
           if constexpr (VB == 0) {
             uint32_t hw = 0;
-            if (ok) hw = static_cast<const uint32_t*>(p.v)[(trow * Dv + d0) / 2];
+            if (ok) {
+              // an element pair in one 4-byte load when Dv is even; else two
+              // loads, the second only inside the row
+              const uint16_t* ve = static_cast<const uint16_t*>(p.v) + trow * Dv + d0;
+              if ((Dv & 1) == 0)
+                hw = *reinterpret_cast<const uint32_t*>(ve);
+              else
+                hw = ve[0] | (d0 + 1 < Dv ? static_cast<uint32_t>(ve[1]) << 16 : 0u);
+            }
             c0[u] = PDT == TQ_DTYPE_BF16 ? bf16_bits_to_f32(hw & 0xffffu) : f16_bits_to_f32(hw & 0xffffu);
             c1[u] = PDT == TQ_DTYPE_BF16 ? bf16_bits_to_f32(hw >> 16) : f16_bits_to_f32(hw >> 16);
           } else {
@@ -862,9 +895,8 @@ int general_attention(const GenCall& c) {
   const bool prod = c.kv_kind == TQ_KV_PROD;
   if (c.B < 0 || c.Hq <= 0 || c.Hkv <= 0 || c.L < 1 || c.Hq % c.Hkv)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: bad heads/L (Hq %d, Hkv %d, L %d)", c.Hq, c.Hkv, c.L);
-  if (c.Dk < 8 || c.Dk > kGenMaxDim || c.Dk % 8 || c.Dv < 8 || c.Dv > kGenMaxDim || c.Dv % 8)
-    return fail(TQ_ERR_UNSUPPORTED, "attention: head dims k %d / v %d (multiples of 8 in 8..512 are built)",
-                c.Dk, c.Dv);
+  if (c.Dk < 8 || c.Dk > kGenMaxDim || c.Dv < 8 || c.Dv > kGenMaxDim)
+    return fail(TQ_ERR_UNSUPPORTED, "attention: head dims k %d / v %d (8..512 are built)", c.Dk, c.Dv);
   if (c.q_dtype != TQ_DTYPE_F32 && c.q_dtype != TQ_DTYPE_F16 && c.q_dtype != TQ_DTYPE_BF16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "attention: q_dtype %d", c.q_dtype);
   if (c.kv_kind != TQ_KV_PACKED && c.kv_kind != TQ_KV_PLAIN && c.kv_kind != TQ_KV_PROD)
@@ -1026,7 +1058,8 @@ int general_attention(const GenCall& c) {
   }
   rc = tile ? launch_tile_partial(p, kb, c.v_bits, st) : launch_gen_partial(p, kb, plain ? 0 : c.v_bits, st);
   if (rc) return rc;
-  if (plain || p.merge_had) {
+  // the flat merge takes 4 value columns per thread: plain values need Dv % 4 == 0
+  if ((plain && c.Dv % 4 == 0) || p.merge_had) {
     const int64_t items = static_cast<int64_t>(c.B) * c.Hkv * (c.Hq / c.Hkv) * c.L * (c.Dv / 4);
     const int64_t pair_items = static_cast<int64_t>(c.Hq / c.Hkv) * c.L * (c.Dv / 4);
     // after the tile kernel, each pair's merge blocks run on the XCD whose

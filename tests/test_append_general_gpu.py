@@ -1,5 +1,5 @@
 """GPU parity of the dense-rotation append and dequantize at the dims the
-fixed-size kernels do not take (multiples of 8 up to 512; the reference picks
+fixed-size kernels do not take (any dim in 8..512; the reference picks
 the dense rotation for every dim that is not a power of two,
 turboquant_cache.py:4122-4139), and of caches built at such dims.
 
@@ -44,7 +44,7 @@ def _check(x_in, bits, d, seed, got_packed, got_norms, norm_dtype="float32"):
     return int(bad.sum())
 
 
-@pytest.mark.parametrize("d", [8, 24, 48, 80, 96, 160, 192, 320, 512])
+@pytest.mark.parametrize("d", [8, 13, 24, 38, 48, 80, 96, 99, 130, 160, 192, 320, 509, 512])
 @pytest.mark.parametrize("xdt", ["bf16", "f16", "f32"])
 def test_dense_append_any_dim(device, d, xdt):
     rng = np.random.default_rng(2000 + d)
@@ -83,7 +83,7 @@ def test_dense_append_f16_norms_and_division_edges(device):
 
 
 @pytest.mark.parametrize("d,rot", [(96, "dense"), (320, "dense"), (512, "hadamard"), (512, "dense"),
-                                   (40, "dense")])
+                                   (40, "dense"), (13, "dense"), (99, "dense"), (130, "dense")])
 def test_dequantize_any_dim(device, d, rot):
     rng = np.random.default_rng(2200 + d)
     bits = 3
@@ -101,7 +101,7 @@ def test_dequantize_any_dim(device, d, rot):
     np.testing.assert_allclose(got.cpu().numpy(), want, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("k_dim,v_dim", [(96, 96), (192, 128), (128, 80)])
+@pytest.mark.parametrize("k_dim,v_dim", [(96, 96), (192, 128), (128, 80), (100, 100), (75, 58)])
 def test_cache_at_other_head_dims(device, k_dim, v_dim):
     """TurboQuantKVCache whose codecs pick the dense rotation for the dims that
     are not powers of two: prefill + decode appends through update_and_fetch,

@@ -264,9 +264,11 @@ def test_dequantize_matches_oracle(device, d, bits):
     np.testing.assert_allclose(got, want, atol=1e-5)
 
 
-def test_plain_append_copies_rows(device):
-    x = torch.randn(2, 4, 5, 128, dtype=torch.float16, device=device)
-    dst = torch.zeros(2, 4, 16, 128, dtype=torch.float16, device=device)
+@pytest.mark.parametrize("d", [128, 100, 13])
+def test_plain_append_copies_rows(device, d):
+    """16-byte copies for dims that are multiples of 8, single elements otherwise."""
+    x = torch.randn(2, 4, 5, d, dtype=torch.float16, device=device)
+    dst = torch.zeros(2, 4, 16, d, dtype=torch.float16, device=device)
     ops.append_plain(x.transpose(1, 2).contiguous().transpose(1, 2), dst, 7)
     assert torch.equal(dst[:, :, 7:12], x)
     assert not dst[:, :, :7].any() and not dst[:, :, 12:].any()

@@ -134,9 +134,12 @@ def test_general_attention_validates_without_the_gpu():
     fake = ctypes.c_void_p(16)
     ok = dict(kcb=fake, k_rot=fake, vcb=fake, v_rot=fake)
     assert lib.tq_attention_general(*_general_args(**ok)) == _lib.TQ_OK  # B = 0
+    # any dim in 8..512 with the dense rotation, odd ones included
+    for kw in (dict(v_dim=100), dict(v_dim=37), dict(k_rot_kind=1, k_dim=99)):
+        assert lib.tq_attention_general(*_general_args(**dict(ok, **kw))) == _lib.TQ_OK, kw
     bad = [
         (dict(k_dim=520), _lib.TQ_ERR_UNSUPPORTED, b"head dims"),
-        (dict(v_dim=100), _lib.TQ_ERR_UNSUPPORTED, b"head dims"),
+        (dict(v_dim=7), _lib.TQ_ERR_UNSUPPORTED, b"head dims"),
         (dict(k_dim=96), _lib.TQ_ERR_INVALID_ARGUMENT, b"power-of-two"),   # Hadamard keys
         (dict(v_rot_kind=0, v_dim=96), _lib.TQ_ERR_INVALID_ARGUMENT, b"power-of-two"),
         (dict(mask_kind=1), _lib.TQ_ERR_INVALID_ARGUMENT, b"mask"),

@@ -72,7 +72,7 @@ def test_head_dim_512_hadamard(device, Hq, Hkv, L, T, kb, vb):
     run_case(device, 500 + 7 * kb + vb + L, 1, Hq, Hkv, L, T, 512, kb, vb)
 
 
-@pytest.mark.parametrize("d", [80, 96, 192, 320, 512])
+@pytest.mark.parametrize("d", [80, 96, 192, 320, 512, 13, 50, 99, 130])
 def test_dense_rotation_other_dims(device, d):
     """Non-power-of-two dims take the dense rotation (turboquant_cache.py:4125-4133);
     d = 512 asks for it explicitly."""
@@ -93,7 +93,9 @@ def test_head_dim_512_left_padding(device):
                                              (192, "dense", 128, "hadamard"),
                                              (64, "hadamard", 96, "dense"),
                                              (128, "hadamard", 128, "dense"),
-                                             (256, "hadamard", 512, "hadamard")])
+                                             (256, "hadamard", 512, "hadamard"),
+                                             (100, "dense", 37, "dense"),
+                                             (64, "hadamard", 130, "dense")])
 def test_key_and_value_dims_differ(device, dk, krot, dv, vrot):
     packed_case(device, 700 + dk + dv, 2, 8, 2, 1, 1700, dk, dv, 3, 2, krot, vrot,
                 lengths=[1700, 900])
@@ -194,7 +196,7 @@ def _plain_case(device, seed, B, Hq, Hkv, L, T, dk, dv, kvdt=torch.float16, mask
     assert_close(out, want, "bf16", f"plain B{B} Hq{Hq} Hkv{Hkv} L{L} T{T} k{dk} v{dv}")
 
 
-@pytest.mark.parametrize("dk,dv", [(512, 512), (96, 96), (192, 128)])
+@pytest.mark.parametrize("dk,dv", [(512, 512), (96, 96), (192, 128), (100, 100), (13, 37), (130, 66)])
 def test_plain_layers_other_dims(device, dk, dv):
     _plain_case(device, 900 + dk + dv, 2, 8, 2, 2, 1300, dk, dv, lengths=[1300, 640])
 
