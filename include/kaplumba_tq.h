@@ -139,7 +139,9 @@ int tq_dequantize(const uint32_t* packed, const void* norms, int norm_dtype,
  *   [B, H, capacity] in norm_dtype.
  * P (projection, dim x dim f32 row-major, 16-byte aligned) is
  * default_rng(seed + 1 + 2971*dim + 17).standard_normal (tq.py:3579-3584).
- * dim in {64, 128, 256}; the workspace (>= tq_prod_workspace_size bytes,
+ * dim a power of two in 32..512 (the sign projection of d = 64 / 128 / 256 on
+ * the matrix cores, of 32 and 512 on the vector ALUs); the workspace
+ * (>= tq_prod_workspace_size bytes,
  * 16-byte aligned) holds the f32 residuals between the two kernels.
  */
 int64_t tq_prod_workspace_size(int B, int H, int L, int dim);

@@ -104,7 +104,9 @@ struct DequantGeneralArgs {
 int launch_dequant_general(const DequantGeneralArgs& a, int64_t n_vec, hipStream_t st);
 
 // The same product for f32 input with a one-bit output (x @ R^T >= 0), the
-// Prod codec's QJL signs; norms receive ||x||.
+// Prod codec's QJL signs; norms receive ||x||.  d = 64 / 128 / 256 on the
+// matrix cores, other dims on the vector ALUs (tq_append_general.hip).
 int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st);
+int launch_append_dense_signs_general(const AppendArgs& a, int dim, hipStream_t st);
 
 }  // namespace tq

@@ -506,7 +506,7 @@ int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st) {
     case 128: return launch_dense_signs_dim<128>(a, st);
     case 256: return launch_dense_signs_dim<256>(a, st);
   }
-  return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d not in {64, 128, 256}", dim);
+  return launch_append_dense_signs_general(a, dim, st);
 }
 
 int launch_append_dense(const AppendArgs& a, int dim, int bits, int x_dtype, hipStream_t st) {

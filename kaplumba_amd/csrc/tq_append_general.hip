@@ -32,7 +32,11 @@ __device__ __forceinline__ int pow2_ceil(int x) {  // x >= 1
   return r;
 }
 
-template <int BITS, int XDT>
+// SGN: the Prod codec's QJL signs instead of indices (BITS = 1, no
+// midpoints): bit = y >= 0 for y = u @ P^T, which has the sign of
+// residual @ P^T (u is the residual over its norm); the norm written is the
+// residual's.
+template <int BITS, int XDT, bool SGN = false>
 __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a, int D) {
   __shared__ float s_u[kGaVec][kGaMaxDim];
   __shared__ uint8_t s_idx[kGaVec][kGaMaxDim];
@@ -50,7 +54,7 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
   // exact zeros)
   const int LP = D <= 32 ? 32 : 32 * pow2_ceil((D + 31) / 32);
   const int NL = LP / 32;
-  if (tid < NMID) s_mid[tid] = a.mid[tid];
+  if (!SGN && tid < NMID) s_mid[tid] = a.mid[tid];
   auto vec_coords = [&](int64_t vec, int& b, int& h, int& l) {
     l = static_cast<int>(vec % a.L);
     const int64_t bh = vec / a.L;
@@ -145,8 +149,12 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
     for (int v = 0; v < kGaVec; ++v) {
       const float y = __fadd_rn(__fadd_rn(acc[v].x, acc[v].y), __fadd_rn(acc[v].z, acc[v].w));
       uint32_t q = 0;
+      if constexpr (SGN) {
+        q = y >= 0.f ? 1u : 0u;
+      } else {
 #pragma unroll
-      for (int m = 0; m < NMID; ++m) q += y > s_mid[m] ? 1u : 0u;
+        for (int m = 0; m < NMID; ++m) q += y > s_mid[m] ? 1u : 0u;
+      }
       s_idx[v][j] = static_cast<uint8_t>(q);
     }
   }
@@ -252,6 +260,15 @@ int launch_append_dense_general(const AppendArgs& a, int dim, int bits, int x_dt
     case 4: return launch_general_bits<4>(a, dim, x_dtype, st);
   }
   return fail(TQ_ERR_INVALID_ARGUMENT, "append: bits %d not in 1..4", bits);
+}
+
+int launch_append_dense_signs_general(const AppendArgs& a, int dim, hipStream_t st) {
+  if (dim < 8 || dim > kGaMaxDim)
+    return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d (8..512)", dim);
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  hipLaunchKernelGGL((append_dense_general_kernel<1, TQ_DTYPE_F32, true>),
+                     dim3(static_cast<unsigned>((n_vec + kGaVec - 1) / kGaVec)), dim3(256), 0, st, a, dim);
+  return check_launch("append_dense_general_kernel (signs)");
 }
 
 int launch_dequant_general(const DequantGeneralArgs& a, int64_t n_vec, hipStream_t st) {

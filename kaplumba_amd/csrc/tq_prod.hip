@@ -9,7 +9,8 @@
 //                         append_rht_kernel), the estimate R^-1(c[idx]) and the
 //                         residual u - estimate, written in f32 to a workspace;
 //   append_dense_kernel   (signs variant) residual @ P^T on the matrix cores
-//                         with one-bit output (>= 0) and ||residual||.
+//                         with one-bit output (>= 0) and ||residual|| (d = 32
+//                         and 512: the general dense kernel's signs mode).
 // Dequantize (:4668-4677): n * (R^-1(c[idx]) + sqrt(pi/2)/D * rn * (s @ P)).
 #include <type_traits>
 
@@ -85,6 +86,7 @@ __device__ __forceinline__ void group_fwht(float (&v)[32], int g) {
   if constexpr (NL >= 2) cross(std::integral_constant<int, 1>{});
   if constexpr (NL >= 4) cross(std::integral_constant<int, 2>{});
   if constexpr (NL >= 8) cross(std::integral_constant<int, 4>{});
+  if constexpr (NL >= 16) cross(std::integral_constant<int, 8>{});
 }
 
 template <int D, int MB, int XDT>
@@ -128,6 +130,7 @@ __global__ __launch_bounds__(256) void prod_residual_kernel(ProdArgs a) {
   if constexpr (NL >= 2) ss = __fadd_rn(ss, xor_lane<1>(ss));
   if constexpr (NL >= 4) ss = __fadd_rn(ss, xor_lane<2>(ss));
   if constexpr (NL >= 8) ss = __fadd_rn(ss, xor_lane<4>(ss));
+  if constexpr (NL >= 16) ss = __fadd_rn(ss, xor_lane<8>(ss));
   const float n = sqrt_rn(ss);
   const float den = fmaxf(n, kNormEps);
   float u[32];
@@ -192,40 +195,50 @@ __device__ __forceinline__ float load_nrm(const void* p, int dt, int64_t i) {
   return dt == TQ_DTYPE_F16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
-// One block of D threads per token vector: thread i forms coordinate i.
+// One block per token vector (min(D, 256) threads); thread i forms
+// coordinates i, i + 256, ... (D a power of two in 32..512).
+constexpr int kProdDqMaxDim = 512;
+
 __global__ __launch_bounds__(256) void prod_dequant_kernel(ProdDequantArgs a) {
-  __shared__ float s_y[256];
-  __shared__ float s_s[256];
-  const int i = threadIdx.x;
+  __shared__ float s_y[kProdDqMaxDim];
+  __shared__ float s_s[kProdDqMaxDim];
+  const int nt = blockDim.x;
   const int64_t vec = blockIdx.x;  // (b * H + h) * T + t
   const int t = static_cast<int>(vec % a.T);
   const int64_t bh = vec / a.T;
   const int64_t row = bh * a.cap + t;
   const int D = a.D;
-  s_s[i] = ((a.sgn[row * (D / 32) + i / 32] >> (i % 32)) & 1u) ? 1.f : -1.f;
-  float mse = 0.f;
-  if (a.mb > 0) {
-    const int pw = D * a.mb / 32;
-    const int pos = i * a.mb;
-    uint32_t idx = a.mse[row * pw + (pos >> 5)] >> (pos & 31);
-    if ((pos & 31) + a.mb > 32) idx |= a.mse[row * pw + (pos >> 5) + 1] << (32 - (pos & 31));
-    s_y[i] = a.cb[idx & ((1u << a.mb) - 1u)];
+  for (int i = threadIdx.x; i < D; i += nt) {
+    s_s[i] = ((a.sgn[row * (D / 32) + i / 32] >> (i % 32)) & 1u) ? 1.f : -1.f;
+    if (a.mb > 0) {
+      const int pw = D * a.mb / 32;
+      const int pos = i * a.mb;
+      uint32_t idx = a.mse[row * pw + (pos >> 5)] >> (pos & 31);
+      if ((pos & 31) + a.mb > 32) idx |= a.mse[row * pw + (pos >> 5) + 1] << (32 - (pos & 31));
+      s_y[i] = a.cb[idx & ((1u << a.mb) - 1u)];
+    }
   }
   __syncthreads();
   if (a.mb > 0) {
+    // butterflies at distance hs: thread k of D / 2 takes the pair (i0, i0 + hs)
     for (int hs = 1; hs < D; hs <<= 1) {
-      const float x0 = s_y[i], x1 = s_y[i ^ hs];
-      __syncthreads();
-      s_y[i] = (i & hs) ? x1 - x0 : x0 + x1;
+      for (int k = threadIdx.x; k < D / 2; k += nt) {
+        const int i0 = (k / hs) * 2 * hs + (k % hs);
+        const float x0 = s_y[i0], x1 = s_y[i0 + hs];
+        s_y[i0] = x0 + x1;
+        s_y[i0 + hs] = x0 - x1;
+      }
       __syncthreads();
     }
-    mse = s_y[i] * a.scale * a.signs[i];
   }
-  float qjl = 0.f;  // (s @ P)[i]
-  for (int j = 0; j < D; ++j) qjl = fmaf(s_s[j], a.proj[static_cast<int64_t>(j) * D + i], qjl);
   const float n = load_nrm(a.norms, a.norm_dtype, row);
   const float rn = load_nrm(a.rnorms, a.norm_dtype, row);
-  a.out[vec * D + i] = n * (mse + a.qjl_scale * rn * qjl);
+  for (int i = threadIdx.x; i < D; i += nt) {
+    const float mse = a.mb > 0 ? s_y[i] * a.scale * a.signs[i] : 0.f;
+    float qjl = 0.f;  // (s @ P)[i]
+    for (int j = 0; j < D; ++j) qjl = fmaf(s_s[j], a.proj[static_cast<int64_t>(j) * D + i], qjl);
+    a.out[vec * D + i] = n * (mse + a.qjl_scale * rn * qjl);
+  }
 }
 
 }  // namespace tq
@@ -277,8 +290,8 @@ extern "C" int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L,
                                 void* stream) {
   if (B < 0 || H < 0 || L < 0) return fail(TQ_ERR_INVALID_ARGUMENT, "prod: negative shape");
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "prod: bits %d not in 1..4", bits);
-  if (dim != 64 && dim != 128 && dim != 256)
-    return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d not in {64, 128, 256}", dim);
+  if (dim < 32 || dim > 512 || (dim & (dim - 1)))
+    return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d (powers of two in 32..512)", dim);
   if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod: norm_dtype %d", norm_dtype);
   if (x_dtype != TQ_DTYPE_F32 && x_dtype != TQ_DTYPE_F16 && x_dtype != TQ_DTYPE_BF16)
@@ -306,9 +319,11 @@ extern "C" int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L,
              static_cast<float*>(workspace)};
   int rc = TQ_OK;
   switch (dim) {
+    case 32: rc = launch_residual<32>(a, mb, x_dtype, st); break;
     case 64: rc = launch_residual<64>(a, mb, x_dtype, st); break;
     case 128: rc = launch_residual<128>(a, mb, x_dtype, st); break;
-    default: rc = launch_residual<256>(a, mb, x_dtype, st); break;
+    case 256: rc = launch_residual<256>(a, mb, x_dtype, st); break;
+    default: rc = launch_residual<512>(a, mb, x_dtype, st); break;
   }
   if (rc) return rc;
   // signs of residual @ P^T and ||residual||, written at the same rows
@@ -339,8 +354,8 @@ extern "C" int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed,
   if (B < 0 || H < 0 || T < 0 || T > capacity)
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: bad shape");
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: bits %d", bits);
-  if (dim != 64 && dim != 128 && dim != 256)
-    return fail(TQ_ERR_UNSUPPORTED, "prod dequantize: dim %d not in {64, 128, 256}", dim);
+  if (dim < 32 || dim > 512 || (dim & (dim - 1)))
+    return fail(TQ_ERR_UNSUPPORTED, "prod dequantize: dim %d (powers of two in 32..512)", dim);
   if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: norm_dtype %d", norm_dtype);
   const int64_t n = static_cast<int64_t>(B) * H * T;
@@ -353,7 +368,7 @@ extern "C" int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed,
                     capacity, signs, mse_codebook, projection,
                     static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim))),
                     static_cast<float>(__builtin_sqrt(3.14159265358979323846 / 2.0) / dim), out};
-  hipLaunchKernelGGL(prod_dequant_kernel, dim3(static_cast<unsigned>(n)), dim3(dim), 0,
+  hipLaunchKernelGGL(prod_dequant_kernel, dim3(static_cast<unsigned>(n)), dim3(dim < 256 ? dim : 256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("prod_dequant_kernel");
 }

@@ -41,8 +41,8 @@ class ProdCodec:
     drawn with ``seed + 1`` and ``scale = sqrt(pi / 2) / dim`` (:4573-4585)."""
 
     def __init__(self, dim: int, bits: int, seed: int):
-        if dim not in (64, 128, 256):
-            raise NotImplementedError(f"Prod codec kernels are built for head dims 64/128/256, got {dim}")
+        if dim < 32 or dim > 512 or dim & (dim - 1):
+            raise NotImplementedError(f"Prod codec kernels are built for power-of-two head dims 32..512, got {dim}")
         if int(bits) != bits or not 1 <= bits <= 4:
             raise ValueError(f"Prod codec bits must be 1..4, got {bits}")
         self.dim = dim

@@ -282,12 +282,19 @@ def test_prod_head_dim_256(device, kb, vb):
     prod_case(device, 1000 + kb * 10 + vb, 1, 8, 2, 1, 1800, 256, kb, vb)
 
 
+@pytest.mark.parametrize("d,kb,vb", [(512, 3, 3), (512, 4, 2), (32, 3, 3), (32, 2, 1)])
+def test_prod_head_dims_32_and_512(device, d, kb, vb):
+    """Prod keys quantized at d = 32 and 512 (the residual kernel's one- and
+    sixteen-lane groups, the general signs projection) and attended over."""
+    prod_case(device, 1040 + d + kb * 10 + vb, 1, 8, 2, 1, 1300, d, kb, vb)
+
+
 def test_prod_many_rows_per_kv_head(device):
     """16 query rows per kv head (GQA 4 x 4 causal drafts)."""
     prod_case(device, 1010, 2, 32, 8, 4, 700, 128, 3, 3, lengths=[700, 333])
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
 def test_prod_one_bit(device, d):
     """1-bit Prod: no MSE part, the score is the QJL term alone."""
     prod_case(device, 1020 + d, 1, 8, 2, 1, 900, d, 1, 3)

@@ -29,7 +29,7 @@ def _oracle(x, codec, norm_dtype):
                            norm_dtype)
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
 def test_prod_quantize_matches_oracle(device, d, bits):
     rng = np.random.default_rng(d + bits)
@@ -90,7 +90,7 @@ def test_prod_quantize_f16_norms_bf16_input(device):
     assert (np.abs(grn - rn) <= np.spacing(rn.astype(np.float16)).astype(np.float32)).all()
 
 
-@pytest.mark.parametrize("d,bits", [(64, 1), (128, 3), (256, 4)])
+@pytest.mark.parametrize("d,bits", [(64, 1), (128, 3), (256, 4), (32, 2), (512, 3), (512, 1)])
 def test_prod_dequantize_matches_oracle(device, d, bits):
     rng = np.random.default_rng(11 + d)
     x = rng.standard_normal((2, 2, 20, d)).astype(np.float32)
