@@ -130,17 +130,22 @@ int tq_dequantize(const uint32_t* packed, const void* norms, int norm_dtype,
  * (array path, tq.py:4653-4666; the fused single-token kernel,
  * tq.py:2968-3116, computes the same quantities): for every vector x,
  *   n = ||x||_2 (f32), u = x / max(n, 1e-6),
- *   idx = MSE indices of u at mb bits (Hadamard rotation with `signs`, the
- *         midpoints and order of tq_append_quantize), packed to mse_packed
- *         [B, H, capacity, dim*mb/32]; with bits == 1 there is no MSE part,
- *   r = u - s * (H(codebook[idx]) / sqrt(dim))   (u when bits == 1),
+ *   idx = MSE indices of u at mb bits (the midpoints and order of
+ *         tq_append_quantize) with the MSE codec's rotation: the Hadamard
+ *         one at power-of-two dims (`signs` = its dim signs), the dense one
+ *         at other dims (`signs` = R, dim x dim row-major, 16-byte aligned),
+ *         as turboquant_cache.py:4122-4139 picks; packed to mse_packed
+ *         [B, H, capacity, ceil(dim*mb/32)]; with bits == 1 no MSE part,
+ *   r = u - R^-1(codebook[idx]): s * (H(codebook[idx]) / sqrt(dim)), or
+ *       codebook[idx] @ R for the dense rotation   (u when bits == 1),
  *   rn = ||r||_2, signs of r @ P^T (1 where >= 0) packed one bit each to
- *   qjl_signs [B, H, capacity, dim/32]; n and rn go to norms / residual_norms
- *   [B, H, capacity] in norm_dtype.
+ *   qjl_signs [B, H, capacity, ceil(dim/32)]; n and rn go to norms /
+ *   residual_norms [B, H, capacity] in norm_dtype.
  * P (projection, dim x dim f32 row-major, 16-byte aligned) is
  * default_rng(seed + 1 + 2971*dim + 17).standard_normal (tq.py:3579-3584).
- * dim a power of two in 32..512 (the sign projection of d = 64 / 128 / 256 on
- * the matrix cores, of 32 and 512 on the vector ALUs); the workspace
+ * dim: powers of two in 32..512, other dims in 8..512 (the sign projection
+ * of d = 64 / 128 / 256 on the matrix cores, of the others on the vector
+ * ALUs; x and its strides 16-byte aligned at the powers of two); the workspace
  * (>= tq_prod_workspace_size bytes,
  * 16-byte aligned) holds the f32 residuals between the two kernels.
  */
@@ -155,8 +160,9 @@ int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L, int dim,
 
 /*
  * Prod dequantize (tq.py:4668-4677), f32 [B, H, T, dim]:
- *   out = n * (s * H(codebook[idx]) / sqrt(dim) + sqrt(pi/2)/dim * rn * (q @ P)),
- * q_j = +1 where sign bit j is set, else -1.
+ *   out = n * (R^-1(codebook[idx]) + sqrt(pi/2)/dim * rn * (q @ P)),
+ * q_j = +1 where sign bit j is set, else -1; R^-1 and `signs` as in
+ * tq_prod_quantize (dims as there).
  */
 int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed, const void* residual_norms,
                        const uint32_t* qjl_signs, int norm_dtype, int B, int H, int T, int dim,

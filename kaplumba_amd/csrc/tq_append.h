@@ -108,5 +108,10 @@ int launch_dequant_general(const DequantGeneralArgs& a, int64_t n_vec, hipStream
 // matrix cores, other dims on the vector ALUs (tq_append_general.hip).
 int launch_append_dense_signs(const AppendArgs& a, int dim, hipStream_t st);
 int launch_append_dense_signs_general(const AppendArgs& a, int dim, hipStream_t st);
+// The Prod codec's MSE part at mb = bits - 1 with the dense rotation (any dim
+// in 8..512): indices to a.packed, ||x|| to a.norms, the residual
+// u - c[idx] @ R to resid [n_vec, dim] f32 (tq_append_general.hip).
+int launch_prod_residual_dense(const AppendArgs& a, int dim, int mb, int x_dtype, float* resid,
+                               const float* cb, hipStream_t st);
 
 }  // namespace tq

@@ -32,18 +32,32 @@ __device__ __forceinline__ int pow2_ceil(int x) {  // x >= 1
   return r;
 }
 
-// SGN: the Prod codec's QJL signs instead of indices (BITS = 1, no
-// midpoints): bit = y >= 0 for y = u @ P^T, which has the sign of
-// residual @ P^T (u is the residual over its norm); the norm written is the
-// residual's.
-template <int BITS, int XDT, bool SGN = false>
-__global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a, int D) {
+// Modes:
+//   kGaQuantize  indices of y = u @ R^T against the midpoints, packed;
+//   kGaSigns     the Prod codec's QJL signs (BITS = 1, no midpoints): bit =
+//                y >= 0 for y = u @ P^T, which has the sign of residual @ P^T
+//                (u is the residual over its norm); the norm written is the
+//                residual's;
+//   kGaProdResid the Prod codec's MSE part at BITS = bits - 1 (0..3) with the
+//                dense rotation (_quantize_unit_with_estimate,
+//                turboquant_cache.py:4151-4166): indices packed as in
+//                kGaQuantize, then the estimate c[idx] @ R (thread j: column
+//                j of R, rows in order, fused multiply-adds) and the residual
+//                u - estimate (u itself when BITS = 0) written to resid
+//                [n_vec, D] f32; norms receive ||x||.
+constexpr int kGaQuantize = 0, kGaSigns = 1, kGaProdResid = 2;
+
+template <int BITS, int XDT, int MODE = kGaQuantize>
+__global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a, int D, float* resid,
+                                                                   const float* cb) {
+  constexpr bool SGN = MODE == kGaSigns;
   __shared__ float s_u[kGaVec][kGaMaxDim];
   __shared__ uint8_t s_idx[kGaVec][kGaMaxDim];
   __shared__ float s_lane[kGaVec][16];
   __shared__ float s_den[kGaVec];
   __shared__ float s_nrm[kGaVec];
   __shared__ float s_mid[16];
+  __shared__ float s_cb[16];
   constexpr int NMID = (1 << BITS) - 1;
   const int tid = threadIdx.x;
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
@@ -55,6 +69,7 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
   const int LP = D <= 32 ? 32 : 32 * pow2_ceil((D + 31) / 32);
   const int NL = LP / 32;
   if (!SGN && tid < NMID) s_mid[tid] = a.mid[tid];
+  if (MODE == kGaProdResid && BITS > 0 && tid < (1 << BITS)) s_cb[tid] = cb[tid];
   auto vec_coords = [&](int64_t vec, int& b, int& h, int& l) {
     l = static_cast<int>(vec % a.L);
     const int64_t bh = vec / a.L;
@@ -113,7 +128,7 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
   // dims read it one element at a time and finish with the D % 4 last
   // coordinates (partial sums 0, 1, 2: u is zero past D in LDS)
   const bool r_vec4 = (D & 3) == 0;
-  for (int j = tid; j < D; j += 256) {
+  for (int j = tid; j < D && !(MODE == kGaProdResid && BITS == 0); j += 256) {
     float4 acc[kGaVec];
 #pragma unroll
     for (int v = 0; v < kGaVec; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -161,14 +176,15 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
   __syncthreads();
   // pack: thread (vector, word)
   const int PW = (D * BITS + 31) / 32;
-  for (int idx = tid; idx < kGaVec * PW; idx += 256) {
+  for (int idx = tid; BITS > 0 && idx < kGaVec * PW; idx += 256) {
     const int v = idx / PW;
     const int w = idx % PW;
     const int64_t vec = vec0 + v;
     if (vec >= n_vec) continue;
     uint32_t word = 0;
-    const int c0 = (32 * w) / BITS;
-    const int c1 = min(D - 1, (32 * w + 31) / BITS);
+    constexpr int BD = BITS > 0 ? BITS : 1;  // (no words at 0 bits)
+    const int c0 = (32 * w) / BD;
+    const int c1 = min(D - 1, (32 * w + 31) / BD);
     for (int c = c0; c <= c1; ++c) {
       const int sh = c * BITS - 32 * w;  // may be negative for a field straddling the word start
       const uint32_t q = s_idx[v][c];
@@ -188,6 +204,24 @@ __global__ __launch_bounds__(256) void append_dense_general_kernel(AppendArgs a,
     else
       static_cast<float*>(a.norms)[row] = s_nrm[tid];
   }
+  if constexpr (MODE == kGaProdResid) {
+    // s_idx is complete (the barrier after the products); u is still in s_u
+    for (int j = tid; j < D; j += 256) {
+      float est[kGaVec];
+#pragma unroll
+      for (int v = 0; v < kGaVec; ++v) est[v] = 0.f;
+      if constexpr (BITS > 0) {
+        for (int i = 0; i < D; ++i) {
+          const float r = a.rot[static_cast<int64_t>(i) * D + j];
+#pragma unroll
+          for (int v = 0; v < kGaVec; ++v) est[v] = __builtin_fmaf(s_cb[s_idx[v][i]], r, est[v]);
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < kGaVec; ++v)
+        if (vec0 + v < n_vec) resid[(vec0 + v) * D + j] = __fsub_rn(s_u[v][j], est[v]);
+    }
+  }
 }
 
 template <int BITS>
@@ -195,9 +229,9 @@ int launch_general_bits(const AppendArgs& a, int dim, int x_dtype, hipStream_t s
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
   const dim3 grid(static_cast<unsigned>((n_vec + kGaVec - 1) / kGaVec));
   switch (x_dtype) {
-    case TQ_DTYPE_F32: hipLaunchKernelGGL((append_dense_general_kernel<BITS, TQ_DTYPE_F32>), grid, dim3(256), 0, st, a, dim); break;
-    case TQ_DTYPE_F16: hipLaunchKernelGGL((append_dense_general_kernel<BITS, TQ_DTYPE_F16>), grid, dim3(256), 0, st, a, dim); break;
-    default: hipLaunchKernelGGL((append_dense_general_kernel<BITS, TQ_DTYPE_BF16>), grid, dim3(256), 0, st, a, dim); break;
+    case TQ_DTYPE_F32: hipLaunchKernelGGL((append_dense_general_kernel<BITS, TQ_DTYPE_F32>), grid, dim3(256), 0, st, a, dim, nullptr, nullptr); break;
+    case TQ_DTYPE_F16: hipLaunchKernelGGL((append_dense_general_kernel<BITS, TQ_DTYPE_F16>), grid, dim3(256), 0, st, a, dim, nullptr, nullptr); break;
+    default: hipLaunchKernelGGL((append_dense_general_kernel<BITS, TQ_DTYPE_BF16>), grid, dim3(256), 0, st, a, dim, nullptr, nullptr); break;
   }
   return check_launch("append_dense_general_kernel");
 }
@@ -266,9 +300,38 @@ int launch_append_dense_signs_general(const AppendArgs& a, int dim, hipStream_t 
   if (dim < 8 || dim > kGaMaxDim)
     return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d (8..512)", dim);
   const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
-  hipLaunchKernelGGL((append_dense_general_kernel<1, TQ_DTYPE_F32, true>),
-                     dim3(static_cast<unsigned>((n_vec + kGaVec - 1) / kGaVec)), dim3(256), 0, st, a, dim);
+  hipLaunchKernelGGL((append_dense_general_kernel<1, TQ_DTYPE_F32, kGaSigns>),
+                     dim3(static_cast<unsigned>((n_vec + kGaVec - 1) / kGaVec)), dim3(256), 0, st, a, dim,
+                     nullptr, nullptr);
   return check_launch("append_dense_general_kernel (signs)");
+}
+
+template <int MB>
+int launch_prod_resid_mb(const AppendArgs& a, int dim, int x_dtype, float* resid, const float* cb,
+                         hipStream_t st) {
+  const int64_t n_vec = static_cast<int64_t>(a.B) * a.H * a.L;
+  const dim3 grid(static_cast<unsigned>((n_vec + kGaVec - 1) / kGaVec));
+  switch (x_dtype) {
+    case TQ_DTYPE_F32: hipLaunchKernelGGL((append_dense_general_kernel<MB, TQ_DTYPE_F32, kGaProdResid>), grid, dim3(256), 0, st, a, dim, resid, cb); break;
+    case TQ_DTYPE_F16: hipLaunchKernelGGL((append_dense_general_kernel<MB, TQ_DTYPE_F16, kGaProdResid>), grid, dim3(256), 0, st, a, dim, resid, cb); break;
+    default: hipLaunchKernelGGL((append_dense_general_kernel<MB, TQ_DTYPE_BF16, kGaProdResid>), grid, dim3(256), 0, st, a, dim, resid, cb); break;
+  }
+  return check_launch("append_dense_general_kernel (prod residual)");
+}
+
+int launch_prod_residual_dense(const AppendArgs& a, int dim, int mb, int x_dtype, float* resid,
+                               const float* cb, hipStream_t st) {
+  if (dim < 8 || dim > kGaMaxDim)
+    return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d (8..512)", dim);
+  if ((reinterpret_cast<uintptr_t>(a.rot) & 15u) != 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "prod: dense rotation matrix must be 16-byte aligned");
+  switch (mb) {
+    case 0: return launch_prod_resid_mb<0>(a, dim, x_dtype, resid, cb, st);
+    case 1: return launch_prod_resid_mb<1>(a, dim, x_dtype, resid, cb, st);
+    case 2: return launch_prod_resid_mb<2>(a, dim, x_dtype, resid, cb, st);
+    case 3: return launch_prod_resid_mb<3>(a, dim, x_dtype, resid, cb, st);
+  }
+  return fail(TQ_ERR_INVALID_ARGUMENT, "prod: bits %d not in 1..4", mb + 1);
 }
 
 int launch_dequant_general(const DequantGeneralArgs& a, int64_t n_vec, hipStream_t st) {

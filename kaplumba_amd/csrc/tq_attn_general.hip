@@ -334,7 +334,8 @@ __global__ __launch_bounds__(kGenThreads) void gen_partial_kernel(GenParams p) {
           }
         }
         uint32_t sw = 0;
-        if constexpr (PROD) sw = tv ? static_cast<const uint32_t*>(p.ksg)[(rowbase + tr) * (Dk / 32) + g] : 0u;
+        // ceil(Dk / 32) sign words per row: group g is word g (G of them)
+        if constexpr (PROD) sw = tv ? static_cast<const uint32_t*>(p.ksg)[(rowbase + tr) * G + g] : 0u;
 #pragma unroll
         for (int j4 = 0; j4 < 8; ++j4) {
           float c[4];
@@ -931,8 +932,8 @@ int general_attention(const GenCall& c) {
     kb = prod ? c.k_bits - 1 : c.k_bits;
     if (kb > 0 && !c.k_codebook) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null key codebook");
     if (prod) {
-      if (c.k_rot_kind != TQ_ROT_HADAMARD || c.Dk < 32)
-        return fail(TQ_ERR_INVALID_ARGUMENT, "attention: Prod keys use the Hadamard rotation (dim >= 32)");
+      if (c.k_rot_kind == TQ_ROT_HADAMARD && c.Dk < 32)
+        return fail(TQ_ERR_INVALID_ARGUMENT, "attention: Prod keys with the Hadamard rotation need dim >= 32");
       if (!c.projection) return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null projection matrix");
       if (c.max_tokens > 0 && (!c.k_signs || !c.k_rnorms))
         return fail(TQ_ERR_INVALID_ARGUMENT, "attention: null Prod key pointer");

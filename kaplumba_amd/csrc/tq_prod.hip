@@ -183,6 +183,8 @@ struct ProdDequantArgs {
   const uint32_t* sgn;
   int norm_dtype;
   int B, H, T, D, mb;
+  int dense;  // MSE rotation: 0 Hadamard (signs = its D signs), 1 dense (signs = R, D x D)
+  int spw;    // sign words per row, ceil(D / 32)
   int64_t cap;
   const float* signs;
   const float* cb;
@@ -196,7 +198,9 @@ __device__ __forceinline__ float load_nrm(const void* p, int dt, int64_t i) {
 }
 
 // One block per token vector (min(D, 256) threads); thread i forms
-// coordinates i, i + 256, ... (D a power of two in 32..512).
+// coordinates i, i + 256, ... (D up to 512; Hadamard: a power of two).  The
+// MSE estimate is R^-1(c[idx]): Hadamard butterflies, or c[idx] @ R for the
+// dense rotation (_rotate_inverse, turboquant_cache.py:4146-4149).
 constexpr int kProdDqMaxDim = 512;
 
 __global__ __launch_bounds__(256) void prod_dequant_kernel(ProdDequantArgs a) {
@@ -209,9 +213,9 @@ __global__ __launch_bounds__(256) void prod_dequant_kernel(ProdDequantArgs a) {
   const int64_t row = bh * a.cap + t;
   const int D = a.D;
   for (int i = threadIdx.x; i < D; i += nt) {
-    s_s[i] = ((a.sgn[row * (D / 32) + i / 32] >> (i % 32)) & 1u) ? 1.f : -1.f;
+    s_s[i] = ((a.sgn[row * a.spw + i / 32] >> (i % 32)) & 1u) ? 1.f : -1.f;
     if (a.mb > 0) {
-      const int pw = D * a.mb / 32;
+      const int pw = (D * a.mb + 31) / 32;
       const int pos = i * a.mb;
       uint32_t idx = a.mse[row * pw + (pos >> 5)] >> (pos & 31);
       if ((pos & 31) + a.mb > 32) idx |= a.mse[row * pw + (pos >> 5) + 1] << (32 - (pos & 31));
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(256) void prod_dequant_kernel(ProdDequantArgs a) {
     }
   }
   __syncthreads();
-  if (a.mb > 0) {
+  if (a.mb > 0 && !a.dense) {
     // butterflies at distance hs: thread k of D / 2 takes the pair (i0, i0 + hs)
     for (int hs = 1; hs < D; hs <<= 1) {
       for (int k = threadIdx.x; k < D / 2; k += nt) {
@@ -234,7 +238,12 @@ __global__ __launch_bounds__(256) void prod_dequant_kernel(ProdDequantArgs a) {
   const float n = load_nrm(a.norms, a.norm_dtype, row);
   const float rn = load_nrm(a.rnorms, a.norm_dtype, row);
   for (int i = threadIdx.x; i < D; i += nt) {
-    const float mse = a.mb > 0 ? s_y[i] * a.scale * a.signs[i] : 0.f;
+    float mse = 0.f;
+    if (a.mb > 0 && a.dense) {
+      for (int d = 0; d < D; ++d) mse = fmaf(s_y[d], a.signs[static_cast<int64_t>(d) * D + i], mse);
+    } else if (a.mb > 0) {
+      mse = s_y[i] * a.scale * a.signs[i];
+    }
     float qjl = 0.f;  // (s @ P)[i]
     for (int j = 0; j < D; ++j) qjl = fmaf(s_s[j], a.proj[static_cast<int64_t>(j) * D + i], qjl);
     a.out[vec * D + i] = n * (mse + a.qjl_scale * rn * qjl);
@@ -290,8 +299,12 @@ extern "C" int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L,
                                 void* stream) {
   if (B < 0 || H < 0 || L < 0) return fail(TQ_ERR_INVALID_ARGUMENT, "prod: negative shape");
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "prod: bits %d not in 1..4", bits);
-  if (dim < 32 || dim > 512 || (dim & (dim - 1)))
-    return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d (powers of two in 32..512)", dim);
+  // powers of two in 32..512: the Hadamard rotation (signs = its dim signs);
+  // other dims in 8..512: the dense one (signs = R, dim x dim), as the MSE
+  // codec picks (turboquant_cache.py:4122-4139)
+  const bool pow2d = (dim & (dim - 1)) == 0;
+  if (dim < 8 || dim > 512 || (pow2d && dim < 32))
+    return fail(TQ_ERR_UNSUPPORTED, "prod: dim %d (8..512; powers of two from 32)", dim);
   if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod: norm_dtype %d", norm_dtype);
   if (x_dtype != TQ_DTYPE_F32 && x_dtype != TQ_DTYPE_F16 && x_dtype != TQ_DTYPE_BF16)
@@ -309,8 +322,8 @@ extern "C" int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L,
     return fail(TQ_ERR_WORKSPACE, "prod: workspace %lld < %lld bytes", (long long)workspace_bytes,
                 (long long)tq_prod_workspace_size(B, H, L, dim));
   const int es = x_dtype == TQ_DTYPE_F32 ? 4 : 2;
-  if (!aligned16p(x) || !aligned16p(workspace) || (x_stride_b * es) % 16 || (x_stride_h * es) % 16 ||
-      (x_stride_l * es) % 16)
+  if (!aligned16p(workspace) || (pow2d && (!aligned16p(x) || (x_stride_b * es) % 16 ||
+                                           (x_stride_h * es) % 16 || (x_stride_l * es) % 16)))
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod: x, its strides and the workspace must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   ProdArgs a{x, x_stride_b, x_stride_h, x_stride_l, B, H, L, signs, mse_midpoints, mse_codebook,
@@ -318,7 +331,25 @@ extern "C" int tq_prod_quantize(const void* x, int x_dtype, int B, int H, int L,
              static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim))),
              static_cast<float*>(workspace)};
   int rc = TQ_OK;
-  switch (dim) {
+  if (!pow2d) {
+    AppendArgs r{};
+    r.x = x;
+    r.sb = x_stride_b;
+    r.sh = x_stride_h;
+    r.sl = x_stride_l;
+    r.B = B;
+    r.H = H;
+    r.L = L;
+    r.rot = signs;
+    r.mid = mse_midpoints;
+    r.packed = mse_packed;
+    r.norms = norms;
+    r.norm_dtype = norm_dtype;
+    r.cap = capacity;
+    r.offset = offset;
+    r.scale = 1.f;
+    rc = launch_prod_residual_dense(r, dim, mb, x_dtype, static_cast<float*>(workspace), mse_codebook, st);
+  } else switch (dim) {
     case 32: rc = launch_residual<32>(a, mb, x_dtype, st); break;
     case 64: rc = launch_residual<64>(a, mb, x_dtype, st); break;
     case 128: rc = launch_residual<128>(a, mb, x_dtype, st); break;
@@ -354,8 +385,9 @@ extern "C" int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed,
   if (B < 0 || H < 0 || T < 0 || T > capacity)
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: bad shape");
   if (bits < 1 || bits > 4) return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: bits %d", bits);
-  if (dim < 32 || dim > 512 || (dim & (dim - 1)))
-    return fail(TQ_ERR_UNSUPPORTED, "prod dequantize: dim %d (powers of two in 32..512)", dim);
+  const bool pow2d = (dim & (dim - 1)) == 0;
+  if (dim < 8 || dim > 512 || (pow2d && dim < 32))
+    return fail(TQ_ERR_UNSUPPORTED, "prod dequantize: dim %d (8..512; powers of two from 32)", dim);
   if (norm_dtype != TQ_DTYPE_F32 && norm_dtype != TQ_DTYPE_F16)
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: norm_dtype %d", norm_dtype);
   const int64_t n = static_cast<int64_t>(B) * H * T;
@@ -365,7 +397,7 @@ extern "C" int tq_prod_dequantize(const void* norms, const uint32_t* mse_packed,
     return fail(TQ_ERR_INVALID_ARGUMENT, "prod dequantize: null pointer");
   if (n > 0x7fffffff) return fail(TQ_ERR_UNSUPPORTED, "prod dequantize: too many vectors");
   ProdDequantArgs a{norms, mse_packed, residual_norms, qjl_signs, norm_dtype, B, H, T, dim, bits - 1,
-                    capacity, signs, mse_codebook, projection,
+                    pow2d ? 0 : 1, (dim + 31) / 32, capacity, signs, mse_codebook, projection,
                     static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(dim))),
                     static_cast<float>(__builtin_sqrt(3.14159265358979323846 / 2.0) / dim), out};
   hipLaunchKernelGGL(prod_dequant_kernel, dim3(static_cast<unsigned>(n)), dim3(dim < 256 ? dim : 256), 0,

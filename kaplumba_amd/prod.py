@@ -37,24 +37,28 @@ class TurboQuantProdState(NamedTuple):
 
 class ProdCodec:
     """``_TurboQuantProdCodec(dim, bits, seed)``: the MSE codec at ``bits - 1``
-    with ``seed`` (Hadamard rotation: power-of-two dims only), the projection
-    drawn with ``seed + 1`` and ``scale = sqrt(pi / 2) / dim`` (:4573-4585)."""
+    with ``seed`` and that codec's own rotation (Hadamard at power-of-two
+    dims, dense otherwise, :4122-4139), the projection drawn with
+    ``seed + 1`` and ``scale = sqrt(pi / 2) / dim`` (:4573-4585)."""
 
     def __init__(self, dim: int, bits: int, seed: int):
-        if dim < 32 or dim > 512 or dim & (dim - 1):
-            raise NotImplementedError(f"Prod codec kernels are built for power-of-two head dims 32..512, got {dim}")
+        pow2 = dim & (dim - 1) == 0
+        if dim < 8 or dim > 512 or (pow2 and dim < 32):
+            raise NotImplementedError(f"Prod codec kernels are built for head dims 8..512 "
+                                      f"(powers of two from 32), got {dim}")
         if int(bits) != bits or not 1 <= bits <= 4:
             raise ValueError(f"Prod codec bits must be 1..4, got {bits}")
         self.dim = dim
         self.bits = int(bits)
         self.seed = seed
         self.mse_bits = self.bits - 1
-        # the rotation signs come from the MSE codec's seed even at 0 MSE bits
-        self.mse_codec = Codec(dim, max(self.mse_bits, 1), seed, "hadamard")
+        # the rotation comes from the MSE codec's seed even at 0 MSE bits
+        self.rotation = "hadamard" if pow2 else "dense"
+        self.mse_codec = Codec(dim, max(self.mse_bits, 1), seed, self.rotation)
         self.projection = cbmod.projection_matrix(dim, seed + 1)
         self.scale = math.sqrt(math.pi / 2) / dim
         self.mse_width = cbmod.packed_width(dim, self.mse_bits)
-        self.sign_width = dim // 32
+        self.sign_width = (dim + 31) // 32
         self._dev: Dict[str, Dict[str, torch.Tensor]] = {}
 
     def device_tensors(self, device) -> Dict[str, torch.Tensor]:
@@ -173,12 +177,13 @@ def attention_prod(queries: torch.Tensor, keys: TurboQuantProdState, v_norms: to
     seq_lens = _seq_array(seq_lens, B, queries.device)
     seq_starts = _seq_array(seq_starts, B, queries.device)
     kt, vt = key_codec.device_tensors(queries.device), value_codec.device_tensors(queries.device)
-    if mask is not None or value_codec.dim != D or value_codec.rotation != "hadamard":
+    if (mask is not None or value_codec.dim != D or value_codec.rotation != "hadamard"
+            or key_codec.rotation != "hadamard"):
         return _attention_general(
             queries, Dv=value_codec.dim, kv_kind=_lib.TQ_KV_PROD, kv_dtype=0,
             k=keys.mse_indices if key_codec.mse_bits > 0 else None, k_norms=keys.norms,
             k_signs=keys.qjl_signs, k_rnorms=keys.residual_norms, k_bits=key_codec.bits,
-            k_codebook=kt["codebook"], k_rot_kind=_lib.TQ_ROT_HADAMARD, k_rot=kt["signs"],
+            k_codebook=kt["codebook"], k_rot_kind=key_codec.mse_codec.rot_kind, k_rot=kt["signs"],
             projection=kt["projection"], v=v_idx, v_norms=v_norms, v_bits=value_codec.bits,
             v_codebook=vt["codebook"], v_rot_kind=value_codec.rot_kind, v_rot=vt["rot"],
             norm_dtype=_lib.torch_dtype_code(v_norms.dtype), cap=cap, T=T, scale=scale,

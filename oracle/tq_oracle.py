@@ -393,15 +393,21 @@ def prod_scale(dim: int) -> np.float32:
 
 
 def quantize_prod(x: np.ndarray, bits: int, signs: np.ndarray, mse_codebook: Optional[np.ndarray],
-                  proj: np.ndarray, norm_dtype: str = "float32"):
+                  proj: np.ndarray, norm_dtype: str = "float32", rot_kind: str = "hadamard",
+                  indices: Optional[np.ndarray] = None):
     """Array path of ``_TurboQuantProdCodec.quantize`` (:4653-4666) in f32.
 
     ``n = ||x||``, ``u = x / max(n, 1e-6)``; the MSE codec at ``bits - 1``
-    quantizes ``u`` (indices as ``quantize_rht``) and its estimate is
-    ``R^-1(c[idx])`` (``_quantize_unit_with_estimate``, :4149-4166); the
-    residual ``u - estimate`` keeps its norm and the signs of
-    ``residual @ P^T`` (``>= 0`` -> 1), packed one bit each.  With
-    ``bits == 1`` there is no MSE part and the residual is ``u``.
+    quantizes ``u`` (indices as ``quantize_rht``, or ``quantize_dense`` when
+    ``rot_kind == "dense"`` and ``signs`` is the rotation R) and its estimate
+    is ``R^-1(c[idx])`` (``_quantize_unit_with_estimate``, :4149-4166):
+    ``_rht_inverse``, or ``c[idx] @ R`` (``_rotate_inverse``, :4146-4149)
+    formed exactly and rounded once to f32; the residual ``u - estimate``
+    keeps its norm and the signs of ``residual @ P^T`` (``>= 0`` -> 1),
+    packed one bit each.  With ``bits == 1`` there is no MSE part and the
+    residual is ``u``.  ``indices`` (tests only) replaces the MSE indices, so
+    that the residual can follow a kernel's indices where a coordinate lies
+    within rounding of a midpoint.
     Returns (norms, mse_packed, residual_norms, sign_packed, projected): the
     f32 ``projected`` lets tests bound sign flips near zero, where the order
     of a matrix product's sum decides.
@@ -411,10 +417,15 @@ def quantize_prod(x: np.ndarray, bits: int, signs: np.ndarray, mse_codebook: Opt
     u = xf / np.maximum(n, EPS)[..., None]
     mb = bits - 1
     if mb >= 1:
-        y = rht_forward_f32(u, signs)
-        idx = quantize_indices(y, midpoints(mse_codebook))
+        dense = rot_kind == "dense"
+        y = rotate_dense_f32(u, signs) if dense else rht_forward_f32(u, signs)
+        idx = quantize_indices(y, midpoints(mse_codebook)) if indices is None else np.asarray(indices)
         mse_packed = pack_lowbit(idx, mb)
-        est = rht_inverse_f32(mse_codebook.astype(np.float32)[idx], signs)
+        c = mse_codebook.astype(np.float32)[idx]
+        if dense:
+            est = (c.astype(np.float64) @ np.asarray(signs, np.float64)).astype(np.float32)
+        else:
+            est = rht_inverse_f32(c, signs)
         residual = (u - est).astype(np.float32)
     else:
         mse_packed = np.zeros((*xf.shape[:-1], 0), np.uint32)
@@ -428,16 +439,18 @@ def quantize_prod(x: np.ndarray, bits: int, signs: np.ndarray, mse_codebook: Opt
 
 def prod_key_vectors(norms, mse_packed, residual_norms, sign_packed, *, bits: int, dim: int,
                      signs: np.ndarray, mse_codebook: Optional[np.ndarray],
-                     proj: np.ndarray) -> np.ndarray:
+                     proj: np.ndarray, rot_kind: str = "hadamard") -> np.ndarray:
     """Dequantized keys ``n * (R^-1 c[idx] + scale * rn * (s @ P))`` in float64
-    (``_TurboQuantProdCodec.dequantize``, :4668-4677), with s = +-1 from the bits."""
+    (``_TurboQuantProdCodec.dequantize``, :4668-4677), with s = +-1 from the
+    bits; ``R^-1 c = c @ R`` for the dense rotation (``signs`` is then R)."""
     n = np.asarray(norms, np.float64)[..., None]
     rn = np.asarray(residual_norms, np.float64)[..., None]
     s = unpack_lowbit(sign_packed, 1, dim).astype(np.float64) * 2.0 - 1.0
     qjl = float(prod_scale(dim)) * rn * (s @ proj.astype(np.float64))
     if bits - 1 >= 1:
         idx = unpack_lowbit(mse_packed, bits - 1, dim)
-        mse = rht_inverse_f64(mse_codebook.astype(np.float64)[idx], signs)
+        c = mse_codebook.astype(np.float64)[idx]
+        mse = c @ np.asarray(signs, np.float64) if rot_kind == "dense" else rht_inverse_f64(c, signs)
     else:
         mse = 0.0
     return n * (mse + qjl)

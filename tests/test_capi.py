@@ -145,7 +145,7 @@ def test_general_attention_validates_without_the_gpu():
         (dict(mask_kind=1), _lib.TQ_ERR_INVALID_ARGUMENT, b"mask"),
         (dict(mask_kind=7, mask=fake, mstrides=fake), _lib.TQ_ERR_INVALID_ARGUMENT, b"mask_kind"),
         (dict(k_bits=5), _lib.TQ_ERR_INVALID_ARGUMENT, b"k_bits"),
-        (dict(kv_kind=_lib.TQ_KV_PROD, k_rot_kind=1), _lib.TQ_ERR_INVALID_ARGUMENT, b"Prod"),
+        (dict(kv_kind=_lib.TQ_KV_PROD, k_dim=16), _lib.TQ_ERR_INVALID_ARGUMENT, b"Prod"),
         (dict(kv_kind=_lib.TQ_KV_PROD), _lib.TQ_ERR_INVALID_ARGUMENT, b"projection"),
         (dict(Hkv=7), _lib.TQ_ERR_INVALID_ARGUMENT, b"heads"),
         (dict(kv_kind=_lib.TQ_KV_PLAIN, kv_dtype=0), _lib.TQ_ERR_INVALID_ARGUMENT, b"plain"),

@@ -254,9 +254,11 @@ def _prod_general_oracle(q, kn, km, kr, ks, vp, vn, kb, vb, d, vd, vr, vrot, qdt
     B, Hq, L, _ = q.shape
     Hkv = kn.shape[1]
     R = Hq // Hkv
-    keys = O.prod_key_vectors(kn, km, kr, ks, bits=kb, dim=d, signs=O.rht_signs(d, 0),
+    pow2 = d & (d - 1) == 0  # the Prod codec's MSE rotation: Hadamard, else dense
+    keys = O.prod_key_vectors(kn, km, kr, ks, bits=kb, dim=d,
+                              signs=O.rht_signs(d, 0) if pow2 else O.rotation_matrix(d, 0),
                               mse_codebook=O.beta_codebook(d, kb - 1) if kb > 1 else None,
-                              proj=O.projection_matrix(d, 1))
+                              proj=O.projection_matrix(d, 1), rot_kind="hadamard" if pow2 else "dense")
     vals = O.dequantize(vp, vn, vb, vd, O.beta_codebook(vd, vb), vrot, vr).astype(np.float64)
     qs = O.scale_queries(q, 1 / math.sqrt(d), qdt).astype(np.float64)
     T = kn.shape[2]
@@ -292,6 +294,14 @@ def test_prod_head_dims_32_and_512(device, d, kb, vb):
 def test_prod_many_rows_per_kv_head(device):
     """16 query rows per kv head (GQA 4 x 4 causal drafts)."""
     prod_case(device, 1010, 2, 32, 8, 4, 700, 128, 3, 3, lengths=[700, 333])
+
+
+@pytest.mark.parametrize("d,kb,vb", [(48, 3, 3), (100, 4, 2), (99, 1, 3), (200, 2, 2)])
+def test_prod_dense_rotation_dims(device, d, kb, vb):
+    """Prod keys at dims that are not powers of two (dense MSE rotation,
+    ceil(d / 32) sign words) with dense values."""
+    prod_case(device, 1100 + d + kb, 1, 8, 2, 1, 900, d, kb, vb, vrot="dense")
+    prod_case(device, 1101 + d + kb, 2, 8, 4, 3, 400, d, kb, vb, vrot="dense", lengths=[400, 151])
 
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256, 512])

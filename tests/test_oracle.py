@@ -374,6 +374,46 @@ def test_prod_quantize_parts_against_closed_forms():
     np.testing.assert_allclose(rn1, 1.0, rtol=1e-6)
 
 
+def test_prod_dense_rotation_reduces_to_the_hadamard_one():
+    """With R = H diag(s) / sqrt(d) -- the Hadamard rotation as a matrix --
+    the dense-rotation Prod (estimate c[idx] @ R) reproduces the Hadamard
+    Prod: the same indices (away from a midpoint), residual norms and signs
+    (away from zero), and the same dequantized keys; an estimate formed as
+    R @ c (transposed) would not."""
+    from scipy.linalg import hadamard
+
+    rng = np.random.default_rng(12)
+    d = 64
+    x = rng.standard_normal((2, 3, 9, d)).astype(np.float32)
+    sg = O.rht_signs(d, 0)
+    Rm = (hadamard(d) * sg[None, :] / np.sqrt(d)).astype(np.float32)   # y = u @ Rm.T = H(s u)/sqrt(d)
+    cb, P = O.beta_codebook(d, 2), O.projection_matrix(d, 1)
+    h = O.quantize_prod(x, 3, sg, cb, P)
+    g = O.quantize_prod(x, 3, Rm, cb, P, rot_kind="dense", indices=O.unpack_lowbit(h[1], 2, d))
+    assert np.array_equal(g[1], h[1]) and np.array_equal(g[0], h[0])
+    np.testing.assert_allclose(g[2], h[2], rtol=1e-5)
+    flip = O.unpack_lowbit(g[3], 1, d) != O.unpack_lowbit(h[3], 1, d)
+    assert (np.abs(h[4][flip]) < 1e-4).all()
+    # the dense indices themselves: equal except within rounding of a midpoint
+    gi = O.quantize_prod(x, 3, Rm, cb, P, rot_kind="dense")[1]
+    assert (O.unpack_lowbit(gi, 2, d) != O.unpack_lowbit(h[1], 2, d)).mean() < 1e-3
+    kw = dict(bits=3, dim=d, mse_codebook=cb, proj=P)
+    kh = O.prod_key_vectors(h[0], h[1], h[2], h[3], signs=sg, **kw)
+    kd = O.prod_key_vectors(h[0], h[1], h[2], h[3], signs=Rm, rot_kind="dense", **kw)
+    np.testing.assert_allclose(kd, kh, rtol=1e-6, atol=1e-6)
+    # a non-symmetric R separates c @ R from R @ c
+    Q = O.rotation_matrix(48, 3)
+    idx = rng.integers(0, 4, size=(5, 48))
+    c = O.beta_codebook(48, 2)
+    xs = rng.standard_normal((5, 48)).astype(np.float32)
+    _, _, rn, _, _ = O.quantize_prod(xs, 3, Q, c, O.projection_matrix(48, 1), rot_kind="dense", indices=idx)
+    u = xs.astype(np.float64) / np.linalg.norm(xs.astype(np.float64), axis=-1, keepdims=True)
+    want = np.linalg.norm(u - c.astype(np.float64)[idx] @ Q.astype(np.float64), axis=-1)
+    wrong = np.linalg.norm(u - c.astype(np.float64)[idx] @ Q.astype(np.float64).T, axis=-1)
+    np.testing.assert_allclose(rn, want, rtol=1e-5)
+    assert np.abs(rn - wrong).max() > 1e-3
+
+
 def test_prod_signs_follow_the_projection_rows():
     """A permutation projection makes the signs the permuted residual's
     signs (catches a transposed P) and ties at zero give 1 (``>= 0``)."""

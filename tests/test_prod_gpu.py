@@ -57,6 +57,68 @@ def test_prod_quantize_matches_oracle(device, d, bits):
     assert not st.qjl_signs.cpu().numpy()[:, :, 4 + L:].any()
 
 
+@pytest.mark.parametrize("d", [48, 99, 100, 200])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_prod_quantize_dense_dims(device, d, bits):
+    """Dims that are not powers of two: the MSE part takes the dense rotation
+    (turboquant_cache.py:4122-4139), estimate c[idx] @ R (:4146-4149).
+    Indices as the dense append's bar (equal except within (d/4 + 4) 2^-24
+    of a midpoint); the residual then follows the kernel's indices.  Its
+    estimate sums d products in f32 where the oracle rounds the exact one
+    once, so residual norms agree within d 2^-22 and signs may flip only
+    within 2^-12 of the row's largest projection."""
+    rng = np.random.default_rng(50 + d + bits)
+    B, H, L = 2, 3, 37
+    x = (rng.standard_normal((B, H, L, d)) * np.exp(rng.normal(0, 0.5, size=(1, H, 1, d)))).astype(np.float16)
+    codec = ProdCodec(d, bits, 0)
+    assert codec.rotation == "dense" and codec.sign_width == (d + 31) // 32
+    st = codec.alloc(B, H, L + 9, device, torch.float32)
+    codec.quantize_into(torch.from_numpy(x).to(device), st, 4)
+    sl = slice(4, 4 + L)
+    xf = x.astype(np.float32)
+    R, P = O.rotation_matrix(d, 0), O.projection_matrix(d, 1)
+    mb = bits - 1
+    cb = O.beta_codebook(d, mb) if mb else None
+    gi = None
+    if mb:
+        wp, _, y = O.quantize_dense(xf, mb, R, cb)
+        gi = O.unpack_lowbit(st.mse_indices.cpu().numpy().astype(np.uint32)[:, :, sl], mb, d).astype(np.int64)
+        wi = O.unpack_lowbit(wp, mb, d).astype(np.int64)
+        bad = gi != wi
+        if bad.any():
+            mids = O.midpoints(cb).astype(np.float64)
+            dist = np.abs(y[bad].astype(np.float64)[:, None] - mids[None, :]).min(axis=1)
+            assert dist.max() <= (d / 4 + 4) * 2.0 ** -24
+            assert np.abs(gi[bad] - wi[bad]).max() == 1
+        assert bad.sum() <= 3
+    n, _, rn, sg, proj = O.quantize_prod(xf, bits, R, cb, P, rot_kind="dense", indices=gi)
+    assert np.array_equal(st.norms.cpu().numpy()[:, :, sl], n)
+    grn = st.residual_norms.cpu().numpy()[:, :, sl]
+    assert np.abs(grn - rn).max() <= d * 2.0 ** -22, float(np.abs(grn - rn).max())
+    gs = O.unpack_lowbit(st.qjl_signs.cpu().numpy().astype(np.uint32)[:, :, sl], 1, d)
+    bad = gs != O.unpack_lowbit(sg, 1, d)
+    scale = np.abs(proj).max(axis=-1, keepdims=True)
+    assert (np.abs(proj)[bad] <= 2.0 ** -12 * np.broadcast_to(scale, proj.shape)[bad]).all()
+    assert bad.sum() <= max(2, bad.size // 2000), int(bad.sum())
+    assert not st.norms.cpu().numpy()[:, :, :4].any()
+    assert not st.qjl_signs.cpu().numpy()[:, :, 4 + L:].any()
+
+
+@pytest.mark.parametrize("d,bits", [(48, 3), (100, 1), (99, 4)])
+def test_prod_dequantize_dense_dims(device, d, bits):
+    rng = np.random.default_rng(13 + d)
+    x = rng.standard_normal((2, 2, 20, d)).astype(np.float32)
+    codec = ProdCodec(d, bits, 1)
+    st = codec.quantize(torch.from_numpy(x).to(device), norm_dtype=torch.float32)
+    got = codec.dequantize(st).cpu().numpy().astype(np.float64)
+    cb = O.beta_codebook(d, bits - 1) if bits > 1 else None
+    want = O.prod_key_vectors(st.norms.cpu().numpy(), st.mse_indices.cpu().numpy().astype(np.uint32),
+                              st.residual_norms.cpu().numpy(), st.qjl_signs.cpu().numpy().astype(np.uint32),
+                              bits=bits, dim=d, signs=O.rotation_matrix(d, 1), mse_codebook=cb,
+                              proj=O.projection_matrix(d, 2), rot_kind="dense")
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
 @pytest.mark.parametrize("bits", [3, 4])
 def test_prod_quantize_division_edge_rows(device, bits):
     # f32 rows on both sides of the quotient method's switch (elements below
