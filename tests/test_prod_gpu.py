@@ -309,3 +309,34 @@ def test_cache_with_prod_keys_decode_and_save_load(device, tmp_path):
     assert loaded.key_quantizer == "prod" and isinstance(loaded.state[0], TurboQuantProdState)
     out2 = loaded.decode_attention(q.to(device), scale=1 / math.sqrt(D))
     assert torch.equal(out, out2)
+
+
+def test_cache_with_prod_keys_at_a_dense_dim(device):
+    """TurboQuantKVCache(key_quantizer="prod") at head dim 100: both codecs take
+    the dense rotation; decode through the model-layer dispatch against the
+    oracle on the cache's own state."""
+    import math
+
+    from kaplumba_amd import TurboQuantKVCache, scaled_dot_product_attention
+    from tests.test_attention_gpu import assert_close
+    from tests.test_general_attention_gpu import _prod_general_oracle
+
+    B, Hq, Hkv, D = 1, 8, 2, 100
+    g = torch.Generator().manual_seed(6)
+    cache = TurboQuantKVCache(bits=3.5, key_quantizer="prod")
+    cache.update_and_fetch(torch.randn(B, Hkv, 260, D, generator=g).to(torch.bfloat16).to(device),
+                           torch.randn(B, Hkv, 260, D, generator=g).to(torch.bfloat16).to(device))
+    kst, vst = cache.update_and_fetch(torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16).to(device),
+                                      torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16).to(device))
+    assert cache.key_codec.rotation == "dense" and cache.value_codec.rotation == "dense"
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    out = scaled_dot_product_attention(q.to(device), kst, vst, cache, 1 / math.sqrt(D), None)
+    ks, vs = cache.state
+    kn, km, kr, ksg = (t.float().cpu().numpy() if t.dtype != torch.uint32 else t.cpu().numpy().astype(np.uint32)
+                       for t in ks)
+    want = _prod_general_oracle(q.float().numpy(), kn, km, kr, ksg, vs.indices.cpu().numpy().astype(np.uint32),
+                                vs.norms.float().cpu().numpy(), 3, 4, D, D, O.rotation_matrix(D, 1), "dense",
+                                "bf16", False, None, None)
+    assert_close(out, want, "bf16", "prod cache at d = 100")
+    kd, vd = cache.dequantize()
+    assert kd.shape == (B, Hkv, 261, D) and vd.shape == (B, Hkv, 261, D)
