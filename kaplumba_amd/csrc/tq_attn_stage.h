@@ -343,8 +343,9 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
 #pragma unroll
   for (int i = 0; i < (1 << VB); ++i) cvb[i] = vcb[i];
   __builtin_amdgcn_s_barrier();
-#pragma unroll
-  for (int k = 0; k < NS; ++k) stage(k, sub_start(k));
+  // the first sub-chunk alone: with every CU requesting only its first
+  // slots, they arrive sooner; the second goes out after the set-up below
+  stage(0, sub_start(0));
 
   // ---- pair tables: hi and lo f16 parts of (c[a] * s, c[b] * s) for key
   // a | b << bits, entry (hi pair, lo pair); keys: REPK replicas, a thread
@@ -390,9 +391,9 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   // The 16 entries of one jj are contiguous, so the lanes' reads of one
   // operand hit distinct banks.
   if (qwave) {
-    // this wave's row and sign loads were issued before its NS * DMA_PER_SLOT
-    // staged loads
-    wait_vmcnt<NS * S::DMA_PER_SLOT>();
+    // this wave's row and sign loads were issued before its first slot's
+    // DMA_PER_SLOT staged loads (loads complete in order for vmcnt)
+    wait_vmcnt<S::DMA_PER_SLOT>();
     STAGE_STAMP(3);
     float y[QE];
 #pragma unroll
@@ -439,6 +440,8 @@ __global__ __launch_bounds__((StageShape<D, KB, VB>::NT), 1) void attn_stage_ker
   }
   lds_only_barrier();
   STAGE_STAMP(5);
+#pragma unroll
+  for (int k = 1; k < NS; ++k) stage(k, sub_start(k));
 
   // ---- lane constants
   const int jq = (n >> 2) & 1;  // token subset of this lane's score column
