@@ -257,7 +257,10 @@ int tq_attention_ranged(const void* q, int q_dtype, int B, int Hq, int Hkv, int 
  * is not read for k_bits == 1).  Dim 64 / 128 with at most 4 query rows per kv
  * head (Hq/Hkv * L) and k_bits >= 2 run the fused row-group kernel; every
  * other shape (power-of-two dims 32..512) runs the kernels of
- * tq_attention_general.  Workspace as tq_attention, sized by
+ * tq_attention_general.  Hadamard rotations on both sides; Prod keys whose
+ * MSE part takes the dense rotation (dims that are not powers of two) go to
+ * tq_attention_general with k_rot_kind TQ_ROT_DENSE.  Workspace as
+ * tq_attention, sized by
  * tq_attention_prod_workspace_size().
  */
 int tq_attention_prod(const void* q, int q_dtype, int B, int Hq, int Hkv, int L, int dim,
@@ -280,14 +283,16 @@ int64_t tq_attention_general_workspace_size(int B, int Hq, int Hkv, int L, int k
 
 /*
  * Attention with the full generality of quantized_attention (tq.py:5110-5203):
- *   - key and value head dims chosen independently (k_dim, v_dim: multiples of
- *     8 in 8..512); q is [B, Hq, L, k_dim], out is contiguous
+ *   - key and value head dims chosen independently (k_dim, v_dim: any dim in
+ *     8..512); q is [B, Hq, L, k_dim], out is contiguous
  *     [B, Hq, L, v_dim] in q_dtype (the output takes value_codec.dim, :5131);
  *   - a rotation kind per side (k_rot_kind, v_rot_kind; Hadamard needs a
  *     power-of-two dim), as each _TurboQuantMSECodec picks its own (:4122-4139);
  *   - kv_kind TQ_KV_PACKED (MSE keys, k_bits 1..4), TQ_KV_PROD (Prod keys of
  *     width k_bits 1..4: k is the MSE part at k_bits - 1 bits, k_signs /
- *     k_residual_norms / projection as tq_attention_prod, Hadamard keys) or
+ *     k_residual_norms / projection as tq_attention_prod; the MSE part's
+ *     rotation per k_rot_kind: Hadamard at power-of-two dims from 32, dense
+ *     at any dim, with ceil(k_dim / 32) sign words per key) or
  *     TQ_KV_PLAIN (k / v [B, Hkv, capacity, dim] in kv_dtype F16/BF16; norms,
  *     codebooks and rotations ignored);
  *   - an optional array mask, applied as _apply_attention_mask
