@@ -393,18 +393,20 @@ struct PlainArgs {
 };
 
 // One thread copies 8 elements (16 bytes); D is a multiple of 8 and the rows
-// are 16-byte aligned.
+// are 16-byte aligned.  Index type I: 32-bit when the piece count fits, so
+// the index divisions are not 64-bit ones.
+template <typename I>
 __global__ __launch_bounds__(256) void append_plain_kernel(PlainArgs a) {
-  const int per_row = a.D / 8;
-  const int64_t total = static_cast<int64_t>(a.B) * a.H * a.L * per_row;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const I per_row = static_cast<I>(a.D / 8);
+  const I total = static_cast<I>(a.B) * a.H * a.L * per_row;
+  const I i = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int c = static_cast<int>(i % per_row);
-  const int64_t vec = i / per_row;
-  const int l = static_cast<int>(vec % a.L);
-  const int64_t bh = vec / a.L;
-  const int h = static_cast<int>(bh % a.H);
-  const int b = static_cast<int>(bh / a.H);
+  const I vec = i / per_row;
+  const int l = static_cast<int>(vec % static_cast<I>(a.L));
+  const I bh = vec / static_cast<I>(a.L);
+  const int h = static_cast<int>(bh % static_cast<I>(a.H));
+  const int b = static_cast<int>(bh / static_cast<I>(a.H));
   const uint4* src = reinterpret_cast<const uint4*>(a.x + b * a.sb + h * a.sh + l * a.sl) + c;
   uint4* dst = reinterpret_cast<uint4*>(
                    a.dst + ((static_cast<int64_t>(b) * a.H + h) * a.cap + a.offset + l) * a.D) +
@@ -674,8 +676,11 @@ extern "C" int tq_append_plain(const void* x, int dtype, int B, int H, int L, in
   if (dim % 8 == 0 && aligned16(x) && aligned16(dst) && (x_stride_b * 2) % 16 == 0 &&
       (x_stride_h * 2) % 16 == 0 && (x_stride_l * 2) % 16 == 0) {
     const int64_t total = static_cast<int64_t>(B) * H * L * (dim / 8);
-    hipLaunchKernelGGL(append_plain_kernel, dim3(static_cast<unsigned>((total + 255) / 256)),
-                       dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    if (total + 256 < (int64_t(1) << 32))
+      hipLaunchKernelGGL(append_plain_kernel<uint32_t>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    else
+      hipLaunchKernelGGL(append_plain_kernel<int64_t>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
     return check_launch("append_plain_kernel");
   }
   const int64_t total = static_cast<int64_t>(B) * H * L * dim;
